@@ -1,0 +1,16 @@
+"""MI355X-native (gfx950) CosyVoice3 Token2Wav DiT estimator: packed CFG batches, hand-written
+HIP kernels behind the C ABI of libfcvdit.so (include/fcv_dit.h).
+
+Public surface (mirrors faster_cosyvoice.token2wav.flashinfer_dit / flashinfer_flow):
+  DiTEstimator            -- the estimator plugin (FlashInferDiT counterpart)
+  solve_euler_packed      -- packed CFG Euler solve, optionally one hipGraph
+  solve_euler_batched     -- padded drop-in of the reference solver
+  apply_mi355x            -- install into a Token2Wav flow (apply_flashinfer counterpart)
+"""
+
+from .estimator import DiTEstimator, rope_tables
+from .solver import apply_mi355x, euler_schedule, solve_euler_batched, solve_euler_packed
+from . import synthetic
+
+__all__ = ["DiTEstimator", "apply_mi355x", "euler_schedule", "rope_tables",
+           "solve_euler_batched", "solve_euler_packed", "synthetic"]

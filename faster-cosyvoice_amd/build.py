@@ -1,0 +1,78 @@
+"""Build libfcvdit.so (gfx950 HIP kernels + C ABI) in-tree with hipcc.
+
+Usage: ``python faster-cosyvoice_amd/build.py`` or ``build_library()`` from Python.
+The shared library lands next to this file so that it travels with the source tree.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+INCLUDE = PKG_DIR.parent / "include"
+LIB_NAME = "libfcvdit.so"
+ARCH = "gfx950"
+
+SOURCES = ["gemm.hip", "attention.hip", "conv.hip", "elementwise.hip", "capi.hip"]
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-result",
+    # packed fp32 VALU forms are kept out of the generated code
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found; the ROCm toolchain is required to build libfcvdit.so")
+    return path
+
+
+def library_path() -> Path:
+    return PKG_DIR / LIB_NAME
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
+    noise = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln and ln.strip()]
+    if noise:
+        sys.stderr.write(f"[{src.name}]\n" + "\n".join(noise) + "\n")
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compile every kernel source for gfx950 and link libfcvdit.so (always rebuilds)."""
+    build_dir = PKG_DIR / "_build"
+    build_dir.mkdir(exist_ok=True)
+    objs = [build_dir / (Path(s).stem + ".o") for s in SOURCES]
+    jobs = min(len(SOURCES), max(1, int(os.environ.get("MAX_JOBS", "8"))))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(lambda so: _compile(CSRC / so[0], so[1]), zip(SOURCES, objs)))
+    out = library_path()
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
+if __name__ == "__main__":
+    build_library(verbose=True)

@@ -1,0 +1,214 @@
+// Varlen flash attention over cu_seqlens for head_dim 64 on gfx950 (MFMA 32x32x16 bf16).
+//
+// One workgroup = one tile of 128 queries of one document x one head; 4 waves x 32 queries.
+// The kernel computes S^T = K Q^T so that the fp32 accumulator of S^T (lane l owns query
+// l%32 and 16 keys) can be rounded in registers and fed straight back as the B operand of
+// O^T = V^T P^T: no LDS round trip for P.  Each lane therefore owns a single query column,
+// so the online-softmax rescale is a per-lane scalar; the row max / row sum need one
+// cross-lane exchange (lane l <-> l^32).
+//
+// K/V tiles of 64 keys go through LDS double buffers: K row-major [key][dim] and V already
+// transposed [dim][key] (the QKV epilogue writes V transposed), both padded to 72 columns.
+// The first key tile starts at the document start rounded down to 8 keys so every 16-byte
+// V^T load is aligned; keys outside [doc start, kv_end) and, in chunk mode, keys in a later
+// chunk than the query are masked to -inf.  No split-KV: each (query, head) is reduced by
+// exactly one wave in key order, so results do not depend on the batch composition.
+#include "kernels.hpp"
+
+namespace fcv {
+namespace {
+
+constexpr int TQ = kAttnTileQ;  // queries per workgroup
+constexpr int TK = 64;          // keys per LDS tile
+constexpr int HD = 64;          // head dim
+constexpr int LDP = 72;         // padded LDS row (bf16 elements)
+
+__global__ __launch_bounds__(256, 2) void attention_kernel(
+    const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ VT,
+    bf16* __restrict__ O, const int32_t* __restrict__ cu, const int32_t* __restrict__ tiles,
+    int rows, int rp, int heads, int chunk, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][TK][LDP];
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][HD][LDP];
+
+  const int tile = blockIdx.x / heads;
+  const int head = blockIdx.x % heads;
+  const int doc = tiles[2 * tile];
+  const int q0 = tiles[2 * tile + 1];
+  const int doc_start = cu[doc];
+  const int doc_end = cu[doc + 1];
+  const int q_last = min(q0 + TQ - 1, doc_end - 1);
+  int kv_end = doc_end;
+  if (chunk > 0) {
+    int lim = ((q_last - doc_start) / chunk + 1) * chunk;
+    kv_end = min(doc_end, doc_start + lim);
+  }
+  const int kv_begin = doc_start & ~7;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int hl = lane >> 5;      // half of the wave
+  const int ql = lane & 31;      // query column owned by this lane
+  const int q_row = q0 + wave * 32 + ql;
+  const int q_pos = q_row - doc_start;
+  // last visible key (exclusive) for this lane's query
+  const int key_lim =
+      chunk > 0 ? min(kv_end, doc_start + (max(q_pos, 0) / chunk + 1) * chunk) : kv_end;
+
+  const bf16* Qh = Q + (long)head * rows * HD;
+  const bf16* Kh = K + (long)head * rows * HD;
+  const bf16* Vh = VT + (long)head * HD * rp;
+
+  // Q^T fragments (B operand): query ql, dims 16*ks + 8*hl + 0..7
+  bf16x8 qf[4];
+  {
+    const int qr = min(q_row, doc_end - 1);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qf[ks] = *reinterpret_cast<const bf16x8*>(Qh + (long)qr * HD + ks * 16 + hl * 8);
+  }
+
+  // tile loaders: each thread moves 2 x 16 bytes of K and 2 x 16 bytes of V^T
+  const int lr = tid >> 3;         // 0..31
+  const int lc = (tid & 7) * 8;    // 0..56
+  bf16x8 rk[2], rv[2];
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      int key = min(kb + lr + 32 * i, rows - 1);
+      rk[i] = *reinterpret_cast<const bf16x8*>(Kh + (long)key * HD + lc);
+      const int d = lr + 32 * i;
+      const int k0 = kb + lc;
+      const bf16* src = Vh + (long)d * rp + k0;
+      if (k0 + 8 <= kv_end) {
+        rv[i] = *reinterpret_cast<const bf16x8*>(src);
+      } else {
+        bf16x8 t;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] = (k0 + e < kv_end) ? src[e] : f2bf(0.0f);
+        rv[i] = t;
+      }
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      *reinterpret_cast<bf16x8*>(&sK[buf][lr + 32 * i][lc]) = rk[i];
+      *reinterpret_cast<bf16x8*>(&sV[buf][lr + 32 * i][lc]) = rv[i];
+    }
+  };
+
+  f32x16 acc_o[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc_o[i][e] = 0.0f;
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+
+  const int n_kt = (kv_end - kv_begin + TK - 1) / TK;
+  fetch(kv_begin);
+  stash(0);
+  __syncthreads();
+
+  for (int it = 0; it < n_kt; ++it) {
+    const int cur = it & 1;
+    const int kb = kv_begin + it * TK;
+    if (it + 1 < n_kt) fetch(kb + TK);
+
+    // S^T[key][query] for two 32-key halves
+    f32x16 s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[kt][e] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[cur][kt * 32 + ql][ks * 16 + hl * 8]);
+        s[kt] = mfma32(kf, qf[ks], s[kt]);
+      }
+    }
+
+    // mask + online softmax (base-2 exponent with the 1/sqrt(64) scale folded in)
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = kb + kt * 32 + (e >> 2) * 8 + hl * 4 + (e & 3);
+        const bool ok = key >= doc_start && key < key_lim;
+        float v = ok ? s[kt][e] * scale_log2 : -INFINITY;
+        s[kt][e] = v;
+        tmax = fmaxf(tmax, v);
+      }
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+    const float m_new = fmaxf(m_run, tmax);
+    const float corr = exp2f(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.0f;
+    bf16x8 pf[4];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float p = exp2f(s[kt][e] - m_new);
+        psum += p;
+        pf[kt * 2 + (e >> 3)][e & 7] = f2bf(p);
+      }
+    }
+    l_run = l_run * corr + psum;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc_o[i][e] *= corr;
+
+    // O^T[d][q] += V^T[d][key] P^T[key][q]; slot j of step s <-> key
+    //   32*(s/2) + 16*(s%2) + 8*(j/4) + 4*hl + j%4  (same rule as the S^T accumulator)
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int kbase = (st >> 1) * 32 + (st & 1) * 16 + hl * 4;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const bf16* vrow = &sV[cur][dt * 32 + ql][0];
+        bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow + kbase);
+        bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + kbase + 8);
+        bf16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        acc_o[dt] = mfma32(vf, pf[st], acc_o[dt]);
+      }
+    }
+
+    if (it + 1 < n_kt) stash(cur ^ 1);
+    __syncthreads();
+  }
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  const float inv = 1.0f / l_tot;
+  if (q_row < doc_end) {
+    bf16* dst = O + (long)q_row * heads * HD + head * HD;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int d = dt * 32 + a * 8 + hl * 4;
+        bf16x4 pk = {f2bf(acc_o[dt][4 * a + 0] * inv), f2bf(acc_o[dt][4 * a + 1] * inv),
+                     f2bf(acc_o[dt][4 * a + 2] * inv), f2bf(acc_o[dt][4 * a + 3] * inv)};
+        *reinterpret_cast<bf16x4*>(dst + d) = pk;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t attention_varlen(const bf16* q, const bf16* k, const bf16* vt, bf16* o,
+                            const int32_t* cu_seqlens, const int32_t* tiles, int n_tiles,
+                            int rows, int rp, int heads, int chunk, hipStream_t stream) {
+  if (n_tiles <= 0) return hipSuccess;
+  const float scale_log2 = 0.125f * 1.4426950408889634f;  // 64^-0.5 * log2(e)
+  hipLaunchKernelGGL(attention_kernel, dim3(n_tiles * heads), dim3(256), 0, stream, q, k, vt, o,
+                     cu_seqlens, tiles, rows, rp, heads, chunk, scale_log2);
+  return hipGetLastError();
+}
+
+}  // namespace fcv

@@ -1,0 +1,426 @@
+// C ABI of libfcvdit.so: handle, layout planning, the packed DiT forward, the CFG Euler
+// step and the hipGraph-captured solve.  See include/fcv_dit.h for the contract.
+#include <algorithm>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/fcv_dit.h"
+#include "kernels.hpp"
+
+using fcv::bf16;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+#define FCV_HIP(expr)                                                                    \
+  do {                                                                                   \
+    hipError_t e_ = (expr);                                                              \
+    if (e_ != hipSuccess)                                                                \
+      return fail(FCV_ERR_RUNTIME, std::string(#expr) + ": " + hipGetErrorString(e_));   \
+  } while (0)
+
+#define FCV_CHECK(cond, code, msg)        \
+  do {                                    \
+    if (!(cond)) return fail(code, msg);  \
+  } while (0)
+
+constexpr size_t kAlign = 256;
+constexpr int kMaxSteps = 64;
+constexpr int kRowTile = 128;
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct Layout {
+  // byte offsets inside the workspace
+  size_t h, nbuf, obuf, q, k, vt, u, ain, vbuf, docid, pos, cu, tiles, mod, tsin, t1, t2, tbuf;
+  size_t total;
+};
+
+Layout make_layout(const FcvDitDims& d, long rows, long n_docs) {
+  const long rp = align_up(std::max<long>(rows, 1), kRowTile);
+  const long n_tiles = rows / fcv::kAttnTileQ + n_docs + 1;
+  const long mod_width = (long)d.depth * 6 * d.dim + 2L * d.dim;
+  Layout L{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off = align_up(off + bytes, kAlign);
+    return at;
+  };
+  L.h = take(rp * d.dim * 4);
+  L.nbuf = take(rp * d.dim * 2);
+  L.obuf = take(rp * d.dim * 2);
+  L.q = take(rp * d.dim * 2);
+  L.k = take(rp * d.dim * 2);
+  L.vt = take(rp * d.dim * 2);
+  L.u = take(rp * (long)d.ff_dim * 2);
+  L.ain = take(rp * 4L * d.mel_dim * 2);
+  L.vbuf = take(rp * (long)d.mel_dim * 4);
+  L.docid = take(rp * 4);
+  L.pos = take(rp * 4);
+  L.cu = take((n_docs + 1) * 4);
+  L.tiles = take(n_tiles * 2 * 4);
+  L.mod = take(std::max<long>(n_docs, 1) * mod_width * 4);
+  L.tsin = take(std::max<long>(n_docs, 1) * 256 * 2);
+  L.t1 = take(std::max<long>(n_docs, 1) * (long)d.dim * 2);
+  L.t2 = take(std::max<long>(n_docs, 1) * (long)d.dim * 2);
+  L.tbuf = take(kMaxSteps * 4);
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+
+struct FcvDit {
+  FcvDitDims dims{};
+  FcvDitWeights w{};
+  long mod_width = 0;
+
+  // plan
+  bool planned = false;
+  unsigned long generation = 0;
+  int rows = 0, rp = 0, n_docs = 0, n_tiles = 0, mask_mode = 0, chunk = 0;
+  std::vector<int32_t> cu_host;
+  char* ws = nullptr;
+  size_t ws_bytes = 0;
+  Layout L{};
+
+  // graph cache
+  hipGraphExec_t graph_exec = nullptr;
+  unsigned long graph_generation = 0;
+  std::vector<uintptr_t> graph_key;
+
+  template <class T>
+  T* at(size_t off) const { return reinterpret_cast<T*>(ws + off); }
+
+  void drop_graph() {
+    if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
+    graph_exec = nullptr;
+    graph_key.clear();
+  }
+};
+
+namespace {
+
+int run_forward(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
+                const float* t, int n_t, float* v_out, hipStream_t s) {
+  const FcvDitDims& d = m->dims;
+  const FcvDitWeights& w = m->w;
+  const int R = m->rows, D = d.dim, F = d.ff_dim, mel = d.mel_dim;
+  const long mod_stride = (n_t == 1) ? 0 : m->mod_width;
+  auto B = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
+
+  float* h = m->at<float>(m->L.h);
+  bf16* nbuf = m->at<bf16>(m->L.nbuf);
+  bf16* obuf = m->at<bf16>(m->L.obuf);
+  bf16* q = m->at<bf16>(m->L.q);
+  bf16* k = m->at<bf16>(m->L.k);
+  bf16* vt = m->at<bf16>(m->L.vt);
+  bf16* u = m->at<bf16>(m->L.u);
+  bf16* ain = m->at<bf16>(m->L.ain);
+  int32_t* docid = m->at<int32_t>(m->L.docid);
+  int32_t* pos = m->at<int32_t>(m->L.pos);
+  int32_t* cu = m->at<int32_t>(m->L.cu);
+  int32_t* tiles = m->at<int32_t>(m->L.tiles);
+  float* mod = m->at<float>(m->L.mod);
+  bf16* tsin = m->at<bf16>(m->L.tsin);
+  bf16* t1 = m->at<bf16>(m->L.t1);
+  bf16* t2 = m->at<bf16>(m->L.t2);
+
+  // timestep embedding -> SiLU(temb) -> every block's AdaLN modulation in one projection
+  // (TimestepEmbedding modules.py:606-616; _project_modulations flashinfer_dit.py:430-445)
+  FCV_HIP(fcv::timestep_sinusoid(t, n_t, 256, tsin, s));
+  FCV_HIP(fcv::gemm_bias_silu_bf16(tsin, 256, B(w.temb_w1), 256, w.temb_b1, n_t, D, 256, t1, D, s));
+  FCV_HIP(fcv::gemm_bias_silu_bf16(t1, D, B(w.temb_w2), D, w.temb_b2, n_t, D, D, t2, D, s));
+  FCV_HIP(fcv::gemm_bias_f32(t2, D, B(w.ada_w), D, w.ada_b, n_t, (int)m->mod_width, D, mod,
+                             (int)m->mod_width, (int)m->mod_width, s));
+
+  // input projection + causal conv position embedding (InputEmbedding dit.py:84-98)
+  FCV_HIP(fcv::pack_inputs(x, cond, mu, spks, docid, R, mel, ain, s));
+  FCV_HIP(fcv::gemm_bias_f32_bf16(ain, 4 * mel, B(w.in_w), 4 * mel, w.in_b, R, D, 4 * mel, h,
+                                  nbuf, D, s));
+  FCV_HIP(fcv::conv_causal_mish(nbuf, D, B(w.conv1_w), w.conv1_b, d.conv_kernel, pos, R, obuf,
+                                nullptr, s));
+  FCV_HIP(fcv::conv_causal_mish(obuf, D, B(w.conv2_w), w.conv2_b, d.conv_kernel, pos, R,
+                                nullptr, h, s));
+
+  // transformer blocks (DiTBlock.forward modules.py:516-530)
+  for (int l = 0; l < d.depth; ++l) {
+    const long base = (long)l * 6 * D;
+    FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 0), (int)(base + D),
+                                     docid, nbuf, s));
+    FCV_HIP(fcv::gemm_qkv_rope(nbuf, D, B(w.qkv_w) + (long)l * 3 * D * D, D,
+                               w.qkv_b + (long)l * 3 * D, R, D, d.heads, pos, w.rope_cos,
+                               w.rope_sin, d.rope_dim, q, k, vt, m->rp, s));
+    FCV_HIP(fcv::attention_varlen(q, k, vt, obuf, cu, tiles, m->n_tiles, R, m->rp, d.heads,
+                                  m->mask_mode == FCV_MASK_CHUNK_CAUSAL ? m->chunk : 0, s));
+    FCV_HIP(fcv::gemm_gated_residual(obuf, D, B(w.out_w) + (long)l * D * D, D,
+                                     w.out_b + (long)l * D, R, D, D, h, D, mod + base + 2 * D,
+                                     mod_stride, docid, s));
+    FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 3 * D),
+                                     (int)(base + 4 * D), docid, nbuf, s));
+    FCV_HIP(fcv::gemm_bias_gelu_bf16(nbuf, D, B(w.ff1_w) + (long)l * F * D, D,
+                                     w.ff1_b + (long)l * F, R, F, D, u, F, s));
+    FCV_HIP(fcv::gemm_gated_residual(u, F, B(w.ff2_w) + (long)l * D * F, F,
+                                     w.ff2_b + (long)l * D, R, D, F, h, D, mod + base + 5 * D,
+                                     mod_stride, docid, s));
+  }
+
+  // final AdaLN (scale, shift) + proj_out (dit.py:174-175, modules.py:260-265)
+  const long fin = (long)d.depth * 6 * D;
+  FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(fin + D), (int)fin, docid,
+                                   nbuf, s));
+  FCV_HIP(fcv::gemm_bias_f32(nbuf, D, B(w.proj_w), D, w.proj_b, R, 128, D, v_out, mel, mel, s));
+  return FCV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fcv_last_error(void) { return g_error.c_str(); }
+
+int fcv_dit_create(const FcvDitDims* dims, const FcvDitWeights* weights, FcvDit** out) {
+  FCV_CHECK(dims && weights && out, FCV_ERR_INVALID, "null argument");
+  const FcvDitDims& d = *dims;
+  FCV_CHECK(d.dim == 1024, FCV_ERR_INVALID, "dim must be 1024");
+  FCV_CHECK(d.dim_head == 64 && d.heads * d.dim_head == d.dim, FCV_ERR_INVALID,
+            "heads * dim_head must equal dim with dim_head 64");
+  FCV_CHECK(d.depth >= 1, FCV_ERR_INVALID, "depth must be >= 1");
+  FCV_CHECK(d.ff_dim > 0 && d.ff_dim % 128 == 0, FCV_ERR_INVALID, "ff_dim must be a multiple of 128");
+  FCV_CHECK(d.mel_dim > 0 && d.mel_dim % 16 == 0 && d.mel_dim <= 128, FCV_ERR_INVALID,
+            "mel_dim must be a multiple of 16 and <= 128");
+  FCV_CHECK(d.conv_groups * 64 == d.dim, FCV_ERR_INVALID, "conv groups must hold 64 channels");
+  FCV_CHECK(d.conv_kernel >= 1 && d.conv_kernel <= 31, FCV_ERR_INVALID, "conv_kernel must be in [1, 31]");
+  FCV_CHECK(d.rope_dim >= 0 && d.rope_dim <= d.dim_head && d.rope_dim % 16 == 0, FCV_ERR_INVALID,
+            "rope_dim must be a multiple of 16 and <= dim_head");
+  FCV_CHECK(d.max_pos >= 1, FCV_ERR_INVALID, "max_pos must be >= 1");
+  const FcvDitWeights& w = *weights;
+  const void* req[] = {w.temb_w1, w.temb_b1, w.temb_w2, w.temb_b2, w.ada_w, w.ada_b, w.in_w,
+                       w.in_b, w.conv1_w, w.conv1_b, w.conv2_w, w.conv2_b, w.qkv_w, w.qkv_b,
+                       w.out_w, w.out_b, w.ff1_w, w.ff1_b, w.ff2_w, w.ff2_b, w.proj_w, w.proj_b,
+                       w.rope_cos, w.rope_sin};
+  for (const void* p : req) FCV_CHECK(p != nullptr, FCV_ERR_INVALID, "null weight pointer");
+  FcvDit* m = new FcvDit();
+  m->dims = d;
+  m->w = w;
+  m->mod_width = (long)d.depth * 6 * d.dim + 2L * d.dim;
+  *out = m;
+  return FCV_OK;
+}
+
+int fcv_dit_destroy(FcvDit* dit) {
+  if (!dit) return FCV_OK;
+  dit->drop_graph();
+  delete dit;
+  return FCV_OK;
+}
+
+size_t fcv_dit_workspace_bytes(const FcvDit* dit, int32_t rows, int32_t n_docs) {
+  if (!dit || rows < 0 || n_docs < 0) return 0;
+  return make_layout(dit->dims, rows, n_docs).total;
+}
+
+int fcv_dit_plan(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask_mode,
+                 int32_t chunk, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
+  FCV_CHECK(cu_host && n_docs >= 1, FCV_ERR_INVALID, "need at least one document");
+  FCV_CHECK(mask_mode == FCV_MASK_FULL || mask_mode == FCV_MASK_CHUNK_CAUSAL, FCV_ERR_INVALID,
+            "mask_mode must be 0 (full) or 1 (chunk-causal)");
+  FCV_CHECK(mask_mode == FCV_MASK_FULL || chunk >= 1, FCV_ERR_INVALID, "chunk must be >= 1");
+  FCV_CHECK(cu_host[0] == 0, FCV_ERR_INVALID, "cu_seqlens[0] must be 0");
+  for (int d = 0; d < n_docs; ++d) {
+    const long len = (long)cu_host[d + 1] - cu_host[d];
+    FCV_CHECK(len >= 1, FCV_ERR_INVALID,
+              "document " + std::to_string(d) + " has length " + std::to_string(len) + " (< 1)");
+    FCV_CHECK(len <= m->dims.max_pos, FCV_ERR_INVALID,
+              "document " + std::to_string(d) + " is longer than max_pos " +
+                  std::to_string(m->dims.max_pos));
+  }
+  const int rows = cu_host[n_docs];
+  FCV_CHECK(rows <= (1 << 24), FCV_ERR_INVALID, "too many rows");
+
+  // attention tiles: (doc, first query row), most expensive first (LPT order)
+  struct T { int doc, q0; long cost; };
+  std::vector<T> tl;
+  for (int d = 0; d < n_docs; ++d) {
+    const int start = cu_host[d], end = cu_host[d + 1];
+    for (int q0 = start; q0 < end; q0 += fcv::kAttnTileQ) {
+      int q_last = std::min(q0 + fcv::kAttnTileQ - 1, end - 1);
+      long kv = end - start;
+      if (mask_mode == FCV_MASK_CHUNK_CAUSAL)
+        kv = std::min<long>(kv, ((q_last - start) / chunk + 1) * (long)chunk);
+      tl.push_back({d, q0, kv});
+    }
+  }
+  std::stable_sort(tl.begin(), tl.end(), [](const T& a, const T& b) { return a.cost > b.cost; });
+  std::vector<int32_t> tiles_host;
+  tiles_host.reserve(tl.size() * 2);
+  for (const T& t : tl) {
+    tiles_host.push_back(t.doc);
+    tiles_host.push_back(t.q0);
+  }
+
+  const Layout L = make_layout(m->dims, rows, n_docs);
+  FCV_CHECK(workspace != nullptr, FCV_ERR_INVALID, "null workspace");
+  FCV_CHECK(workspace_bytes >= L.total, FCV_ERR_INVALID,
+            "workspace too small: need " + std::to_string(L.total) + " bytes, got " +
+                std::to_string(workspace_bytes));
+  FCV_CHECK(reinterpret_cast<uintptr_t>(workspace) % kAlign == 0, FCV_ERR_INVALID,
+            "workspace must be 256-byte aligned");
+
+  m->drop_graph();
+  m->planned = false;
+  m->ws = static_cast<char*>(workspace);
+  m->ws_bytes = workspace_bytes;
+  m->L = L;
+  m->rows = rows;
+  m->rp = (int)align_up(std::max(rows, 1), kRowTile);
+  m->n_docs = n_docs;
+  m->n_tiles = (int)tl.size();
+  m->mask_mode = mask_mode;
+  m->chunk = mask_mode == FCV_MASK_CHUNK_CAUSAL ? chunk : 0;
+  m->cu_host.assign(cu_host, cu_host + n_docs + 1);
+
+  FCV_HIP(hipMemcpyAsync(m->at<int32_t>(L.cu), cu_host, (n_docs + 1) * sizeof(int32_t),
+                         hipMemcpyHostToDevice, s));
+  FCV_HIP(hipMemcpyAsync(m->at<int32_t>(L.tiles), tiles_host.data(),
+                         tiles_host.size() * sizeof(int32_t), hipMemcpyHostToDevice, s));
+  FCV_HIP(fcv::build_row_index(m->at<int32_t>(L.cu), n_docs, rows, m->at<int32_t>(L.docid),
+                               m->at<int32_t>(L.pos), s));
+  FCV_HIP(hipStreamSynchronize(s));
+  m->planned = true;
+  m->generation++;
+  return FCV_OK;
+}
+
+int fcv_dit_plan_info(const FcvDit* m, int32_t* rows, int32_t* n_docs, int32_t* n_tiles) {
+  FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
+  FCV_CHECK(m->planned, FCV_ERR_STATE, "no layout planned");
+  if (rows) *rows = m->rows;
+  if (n_docs) *n_docs = m->n_docs;
+  if (n_tiles) *n_tiles = m->n_tiles;
+  return FCV_OK;
+}
+
+int fcv_dit_forward(FcvDit* m, const float* x, const float* mu, const float* cond,
+                    const float* spks, const float* t, int32_t n_t, float* v_out,
+                    hipStream_t s) {
+  FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
+  FCV_CHECK(m->planned, FCV_ERR_STATE, "fcv_dit_forward called before fcv_dit_plan");
+  FCV_CHECK(x && mu && cond && spks && t && v_out, FCV_ERR_INVALID,
+            "spks and cond are required (null input pointer)");
+  FCV_CHECK(n_t == 1 || n_t == m->n_docs, FCV_ERR_INVALID, "n_t must be 1 or n_docs");
+  return run_forward(m, x, mu, cond, spks, t, n_t, v_out, s);
+}
+
+static int check_cfg_layout(const FcvDit* m) {
+  FCV_CHECK(m->n_docs % 2 == 0, FCV_ERR_INVALID, "CFG batch needs an even number of documents");
+  const int half = m->n_docs / 2;
+  for (int d = 0; d < half; ++d) {
+    FCV_CHECK(m->cu_host[d + 1] - m->cu_host[d] == m->cu_host[half + d + 1] - m->cu_host[half + d],
+              FCV_ERR_INVALID, "CFG halves must have equal document lengths");
+  }
+  return FCV_OK;
+}
+
+int fcv_euler_cfg_step(FcvDit* m, float* x, const float* v, float dt, float cfg, hipStream_t s) {
+  FCV_CHECK(m && x && v, FCV_ERR_INVALID, "null argument");
+  FCV_CHECK(m->planned, FCV_ERR_STATE, "no layout planned");
+  int rc = check_cfg_layout(m);
+  if (rc != FCV_OK) return rc;
+  FCV_HIP(fcv::euler_cfg_update(x, v, m->rows / 2, m->dims.mel_dim, dt, cfg, s));
+  return FCV_OK;
+}
+
+int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const float* spks,
+                  const float* t_host, const float* dt_host, int32_t n_steps, float cfg,
+                  int32_t use_graph, hipStream_t s) {
+  FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
+  FCV_CHECK(m->planned, FCV_ERR_STATE, "fcv_dit_solve called before fcv_dit_plan");
+  FCV_CHECK(x && mu && cond && spks && t_host && dt_host, FCV_ERR_INVALID, "null argument");
+  FCV_CHECK(n_steps >= 1 && n_steps <= kMaxSteps, FCV_ERR_INVALID, "n_steps must be in [1, 64]");
+  int rc = check_cfg_layout(m);
+  if (rc != FCV_OK) return rc;
+
+  float* tbuf = m->at<float>(m->L.tbuf);
+  float* vbuf = m->at<float>(m->L.vbuf);
+  const int rcond = m->rows / 2, mel = m->dims.mel_dim;
+  FCV_HIP(hipMemcpyAsync(tbuf, t_host, n_steps * sizeof(float), hipMemcpyHostToDevice, s));
+
+  auto body = [&]() -> int {
+    for (int step = 0; step < n_steps; ++step) {
+      int r = run_forward(m, x, mu, cond, spks, tbuf + step, 1, vbuf, s);
+      if (r != FCV_OK) return r;
+      FCV_HIP(fcv::euler_cfg_update(x, vbuf, rcond, mel, dt_host[step], cfg, s));
+    }
+    return FCV_OK;
+  };
+  if (!use_graph) return body();
+
+  std::vector<uintptr_t> key = {m->generation, (uintptr_t)x, (uintptr_t)mu, (uintptr_t)cond,
+                                (uintptr_t)spks, (uintptr_t)n_steps};
+  uint32_t bits;
+  std::memcpy(&bits, &cfg, 4);
+  key.push_back(bits);
+  for (int i = 0; i < n_steps; ++i) {
+    std::memcpy(&bits, &dt_host[i], 4);
+    key.push_back(bits);
+  }
+  if (!m->graph_exec || key != m->graph_key) {
+    m->drop_graph();
+    FCV_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    int r = body();
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &graph);
+    if (r != FCV_OK) {
+      if (graph) (void)hipGraphDestroy(graph);
+      return r;
+    }
+    if (e != hipSuccess)
+      return fail(FCV_ERR_RUNTIME, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+    e = hipGraphInstantiate(&m->graph_exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) {
+      m->graph_exec = nullptr;
+      return fail(FCV_ERR_RUNTIME, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    }
+    m->graph_key = key;
+  }
+  FCV_HIP(hipGraphLaunch(m->graph_exec, s));
+  return FCV_OK;
+}
+
+int fcv_pack_padded(FcvDit* m, const float* src, int32_t batch, int32_t channels,
+                    int32_t padded_len, float* dst, hipStream_t s) {
+  FCV_CHECK(m && src && dst, FCV_ERR_INVALID, "null argument");
+  FCV_CHECK(m->planned, FCV_ERR_STATE, "no layout planned");
+  FCV_CHECK(batch == m->n_docs, FCV_ERR_INVALID, "batch must equal the planned document count");
+  for (int d = 0; d < m->n_docs; ++d)
+    FCV_CHECK(m->cu_host[d + 1] - m->cu_host[d] <= padded_len, FCV_ERR_INVALID,
+              "document longer than padded_len");
+  FCV_HIP(fcv::pack_padded(src, batch, channels, padded_len, m->at<int32_t>(m->L.cu),
+                           m->at<int32_t>(m->L.docid), m->at<int32_t>(m->L.pos), m->rows, dst, s));
+  return FCV_OK;
+}
+
+int fcv_unpack_padded(FcvDit* m, const float* src, int32_t batch, int32_t channels,
+                      int32_t padded_len, float* dst, hipStream_t s) {
+  FCV_CHECK(m && src && dst, FCV_ERR_INVALID, "null argument");
+  FCV_CHECK(m->planned, FCV_ERR_STATE, "no layout planned");
+  FCV_CHECK(batch == m->n_docs, FCV_ERR_INVALID, "batch must equal the planned document count");
+  for (int d = 0; d < m->n_docs; ++d)
+    FCV_CHECK(m->cu_host[d + 1] - m->cu_host[d] <= padded_len, FCV_ERR_INVALID,
+              "document longer than padded_len");
+  FCV_HIP(fcv::unpack_padded(src, batch, channels, padded_len, m->at<int32_t>(m->L.cu), dst, s));
+  return FCV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+// Shared device helpers for the gfx950 DiT estimator kernels.
+//
+// Conventions used by every kernel in this library:
+//   * bf16 tensors are stored as raw 16-bit words (type `bf16` below);
+//   * the residual stream and all boundary tensors are fp32;
+//   * MFMA fragments follow the CDNA 16x16 / 32x32 accumulator layouts:
+//       16x16x32 : lane l holds D[4*(l/16) + j][l%16], j = 0..3
+//       32x32x16 : lane l holds D[8*(i/4) + 4*(l/32) + i%4][l%32], i = 0..15
+//     Operand slots are loaded with the same (lane, slot) -> k rule for A and
+//     B, so the result does not depend on the hardware's k order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fcv {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf2f(bf16 v) { return (float)v; }
+__device__ __forceinline__ bf16 f2bf(float v) { return (bf16)v; }
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// tanh-approximated GELU (torch nn.GELU(approximate="tanh")).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+  const float k1 = 0.044715f;
+  float u = k0 * (x + k1 * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(u));
+}
+
+// Mish: x * tanh(softplus(x)), softplus with torch's threshold of 20.
+__device__ __forceinline__ float mish(float x) {
+  float sp = x > 20.0f ? x : log1pf(expf(x));
+  return x * tanhf(sp);
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+}  // namespace fcv

@@ -1,0 +1,205 @@
+// Bandwidth-bound kernels of the DiT estimator path: LayerNorm + AdaLN modulation, packed
+// row index, input packing, timestep sinusoid, the CFG Euler update, and the padded <->
+// packed conversions of the drop-in estimator call.
+#include "kernels.hpp"
+
+namespace fcv {
+namespace {
+
+// One wave per row; each lane owns C/256 float4 groups at stride 256 columns, so every
+// load/store instruction of the wave covers a contiguous 1 KB (fp32) / 512 B (bf16) span.
+// Two-pass statistics from registers (mean, then centered variance), eps 1e-6, biased var.
+template <int C>
+__global__ __launch_bounds__(256) void ln_mod_kernel(const float* __restrict__ h, int rows,
+                                                     const float* __restrict__ mod,
+                                                     long mod_stride, int shift_off,
+                                                     int scale_off,
+                                                     const int32_t* __restrict__ docid,
+                                                     bf16* __restrict__ out) {
+  constexpr int G = C / 256;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float4* src = reinterpret_cast<const float4*>(h + (long)row * C);
+  float4 v[G];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    v[i] = src[lane + 64 * i];
+    s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+  }
+  const float mean = wave_sum(s) * (1.0f / C);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+    ss += (a * a + b * b) + (c * c + d * d);
+  }
+  const float rstd = rsqrtf(wave_sum(ss) * (1.0f / C) + 1e-6f);
+  const float* m = mod + (long)docid[row] * mod_stride;
+  const float4* shift = reinterpret_cast<const float4*>(m + shift_off);
+  const float4* scale = reinterpret_cast<const float4*>(m + scale_off);
+  bf16x4* dst = reinterpret_cast<bf16x4*>(out + (long)row * C);
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int c4 = lane + 64 * i;
+    const float4 sh = shift[c4], sc = scale[c4];
+    bf16x4 o = {f2bf((v[i].x - mean) * rstd * sc.x + sh.x), f2bf((v[i].y - mean) * rstd * sc.y + sh.y),
+                f2bf((v[i].z - mean) * rstd * sc.z + sh.z), f2bf((v[i].w - mean) * rstd * sc.w + sh.w)};
+    dst[c4] = o;
+  }
+}
+
+__global__ void row_index_kernel(const int32_t* __restrict__ cu, int n_docs, int rows,
+                                 int32_t* __restrict__ docid, int32_t* __restrict__ pos) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  int lo = 0, hi = n_docs - 1;  // last doc with cu[doc] <= r
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (cu[mid] <= r) lo = mid; else hi = mid - 1;
+  }
+  docid[r] = lo;
+  pos[r] = r - cu[lo];
+}
+
+// one thread per 8 output columns
+__global__ void pack_inputs_kernel(const float* __restrict__ x, const float* __restrict__ cond,
+                                   const float* __restrict__ mu, const float* __restrict__ spks,
+                                   const int32_t* __restrict__ docid, int rows, int mel,
+                                   bf16* __restrict__ a) {
+  const int per_row = (4 * mel) / 8;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)rows * per_row) return;
+  const int r = (int)(idx / per_row);
+  const int c = (int)(idx % per_row) * 8;
+  const int seg = c / mel, off = c % mel;
+  const float* src;
+  if (seg == 0) src = x + (long)r * mel;
+  else if (seg == 1) src = cond + (long)r * mel;
+  else if (seg == 2) src = mu + (long)r * mel;
+  else src = spks + (long)docid[r] * mel;
+  const float4 u = *reinterpret_cast<const float4*>(src + off);
+  const float4 w = *reinterpret_cast<const float4*>(src + off + 4);
+  bf16x8 o = {f2bf(u.x), f2bf(u.y), f2bf(u.z), f2bf(u.w), f2bf(w.x), f2bf(w.y), f2bf(w.z), f2bf(w.w)};
+  *reinterpret_cast<bf16x8*>(a + (long)r * 4 * mel + c) = o;
+}
+
+__global__ void sinusoid_kernel(const float* __restrict__ t, int n_t, int dim,
+                                bf16* __restrict__ out) {
+  const int m = blockIdx.x;
+  const int half = dim / 2;
+  const float step = (float)(9.210340371976184 / (double)(half - 1));  // ln(1e4)/(half-1)
+  const float scaled_t = 1000.0f * t[m];
+  for (int i = threadIdx.x; i < half; i += blockDim.x) {
+    const float f = expf((float)i * -step);
+    const float arg = scaled_t * f;
+    out[(long)m * dim + i] = f2bf(sinf(arg));
+    out[(long)m * dim + half + i] = f2bf(cosf(arg));
+  }
+}
+
+__global__ void euler_cfg_kernel(float* __restrict__ x, const float* __restrict__ v, int rc,
+                                 int mel, float dt, float cfg) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long n = (long)rc * mel;
+  if (i >= n) return;
+  const float d = (1.0f + cfg) * v[i] - cfg * v[i + n];
+  const float y = x[i] + dt * d;
+  x[i] = y;
+  x[i + n] = y;
+}
+
+// dst[r, c] = src[doc(r), c, pos(r)]
+__global__ void pack_padded_kernel(const float* __restrict__ src, int channels, int padded_len,
+                                   const int32_t* __restrict__ docid,
+                                   const int32_t* __restrict__ pos, int rows,
+                                   float* __restrict__ dst) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)rows * channels) return;
+  const int r = (int)(i / channels), c = (int)(i % channels);
+  dst[i] = src[((long)docid[r] * channels + c) * padded_len + pos[r]];
+}
+
+// dst[b, c, t] = t < len_b ? src[cu[b] + t, c] : 0
+__global__ void unpack_padded_kernel(const float* __restrict__ src, int batch, int channels,
+                                     int padded_len, const int32_t* __restrict__ cu,
+                                     float* __restrict__ dst) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)batch * channels * padded_len) return;
+  const int t = (int)(i % padded_len);
+  const long bc = i / padded_len;
+  const int c = (int)(bc % channels), b = (int)(bc / channels);
+  const int start = cu[b], len = cu[b + 1] - start;
+  dst[i] = t < len ? src[(long)(start + t) * channels + c] : 0.0f;
+}
+
+inline unsigned blocks_for(long n, int threads) { return (unsigned)((n + threads - 1) / threads); }
+
+}  // namespace
+
+hipError_t layer_norm_modulate(const float* h, int C, int rows, const float* mod, long mod_stride,
+                               int shift_off, int scale_off, const int32_t* docid, bf16* out,
+                               hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  if (C != 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(ln_mod_kernel<1024>, dim3(blocks_for(rows, 4)), dim3(256), 0, stream, h,
+                     rows, mod, mod_stride, shift_off, scale_off, docid, out);
+  return hipGetLastError();
+}
+
+hipError_t build_row_index(const int32_t* cu_seqlens, int n_docs, int rows, int32_t* docid,
+                           int32_t* pos, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(row_index_kernel, dim3(blocks_for(rows, 256)), dim3(256), 0, stream,
+                     cu_seqlens, n_docs, rows, docid, pos);
+  return hipGetLastError();
+}
+
+hipError_t pack_inputs(const float* x, const float* cond, const float* mu, const float* spks,
+                       const int32_t* docid, int rows, int mel, bf16* a, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  if (mel % 8 != 0) return hipErrorInvalidValue;
+  const long n = (long)rows * (4 * mel / 8);
+  hipLaunchKernelGGL(pack_inputs_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, x, cond,
+                     mu, spks, docid, rows, mel, a);
+  return hipGetLastError();
+}
+
+hipError_t timestep_sinusoid(const float* t, int n_t, int dim, bf16* out, hipStream_t stream) {
+  if (n_t <= 0) return hipSuccess;
+  hipLaunchKernelGGL(sinusoid_kernel, dim3(n_t), dim3(128), 0, stream, t, n_t, dim, out);
+  return hipGetLastError();
+}
+
+hipError_t euler_cfg_update(float* x, const float* v, int rc, int mel, float dt, float cfg,
+                            hipStream_t stream) {
+  const long n = (long)rc * mel;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(euler_cfg_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, x, v, rc,
+                     mel, dt, cfg);
+  return hipGetLastError();
+}
+
+hipError_t pack_padded(const float* src, int batch, int channels, int padded_len,
+                       const int32_t* cu_seqlens, const int32_t* docid, const int32_t* pos,
+                       int rows, float* dst, hipStream_t stream) {
+  (void)batch;
+  (void)cu_seqlens;
+  const long n = (long)rows * channels;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(pack_padded_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, src,
+                     channels, padded_len, docid, pos, rows, dst);
+  return hipGetLastError();
+}
+
+hipError_t unpack_padded(const float* src, int batch, int channels, int padded_len,
+                         const int32_t* cu_seqlens, float* dst, hipStream_t stream) {
+  const long n = (long)batch * channels * padded_len;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(unpack_padded_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, src,
+                     batch, channels, padded_len, cu_seqlens, dst);
+  return hipGetLastError();
+}
+
+}  // namespace fcv

@@ -1,0 +1,90 @@
+// Host-side launchers of the gfx950 DiT estimator kernels (one .hip file per kernel family).
+// All launchers are asynchronous on `stream` and return hipGetLastError() of the launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.hpp"
+
+namespace fcv {
+
+// ---- GEMM: C[M,N] = A[M,K] . W[N,K]^T (+ bias) with a fused epilogue -------------------
+// Requirements checked by the caller: N % 128 == 0, K % 64 == 0, lda/ldw % 8 == 0.
+
+// out_f32[r, c] = acc + bias[c];  out_bf16[r, c] = bf16(same)   (input projection)
+hipError_t gemm_bias_f32_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
+                              int M, int N, int K, float* out_f32, bf16* out_bf16, int ldo,
+                              hipStream_t stream);
+
+// out[r, c] = acc + bias[c] for c < n_valid (fp32; proj_out, AdaLN projection)
+hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
+                         int M, int N, int K, float* out, int ldo, int n_valid, hipStream_t stream);
+
+// out[r, c] = bf16(silu(acc + bias[c]))   (timestep MLP)
+hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
+                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream);
+
+// out[r, c] = bf16(gelu_tanh(acc + bias[c]))   (FF1)
+hipError_t gemm_bias_gelu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
+                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream);
+
+// h[r, c] += gate[c] * (acc + bias[c]), gate row = mod + docid[r] * mod_stride + gate_off
+// (out-projection and FF2 gated residuals)
+hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
+                               int M, int N, int K, float* h, int ldh, const float* mod,
+                               long mod_stride, const int32_t* docid, hipStream_t stream);
+
+// Fused QKV projection: bias, interleaved RoPE on columns [0, rope_dim) of q and k
+// (angles from cos/sin tables [max_pos][rope_dim/2], row position from pos[r]),
+// scatter to q, k : [heads][M][dim_head] and vt : [heads][dim_head][rp] (V transposed).
+hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const float* bias, int M,
+                         int dim, int heads, const int32_t* pos, const float* rope_cos,
+                         const float* rope_sin, int rope_dim, bf16* q, bf16* k, bf16* vt, int rp,
+                         hipStream_t stream);
+
+// ---- attention ----------------------------------------------------------------------------
+// Varlen attention over cu_seqlens, head_dim 64. tiles[i] = {doc, first query row}.
+// chunk == 0: full attention inside each document; chunk > 0: key visible iff
+// (key_pos / chunk) <= (query_pos / chunk).
+hipError_t attention_varlen(const bf16* q, const bf16* k, const bf16* vt, bf16* o,
+                            const int32_t* cu_seqlens, const int32_t* tiles, int n_tiles, int rows,
+                            int rp, int heads, int chunk, hipStream_t stream);
+constexpr int kAttnTileQ = 128;
+
+// ---- causal grouped conv position embedding (64 channels per group) -------------------------
+// y[r, g*64+co] = mish(bias + sum_{j,ci} W[g][j][co][ci] x[r-(taps-1)+j, g*64+ci]), rows before
+// the row's document start read as zero.  out_bf16 != null: store y;  h != null: h += y.
+hipError_t conv_causal_mish(const bf16* x, int C, const bf16* w, const float* bias, int taps,
+                            const int32_t* pos, int rows, bf16* out_bf16, float* h,
+                            hipStream_t stream);
+
+// ---- bandwidth-bound kernels -----------------------------------------------------------------
+// out[r, :] = bf16(LN(h[r, :]) * scale + shift), scale/shift rows = mod + docid[r]*mod_stride + off
+hipError_t layer_norm_modulate(const float* h, int C, int rows, const float* mod, long mod_stride,
+                               int shift_off, int scale_off, const int32_t* docid, bf16* out,
+                               hipStream_t stream);
+
+// docid[r], pos[r] from device cu_seqlens[n_docs+1].
+hipError_t build_row_index(const int32_t* cu_seqlens, int n_docs, int rows, int32_t* docid,
+                           int32_t* pos, hipStream_t stream);
+
+// a[r, 0:4*mel] = bf16([x[r], cond[r], mu[r], spks[docid[r]]])
+hipError_t pack_inputs(const float* x, const float* cond, const float* mu, const float* spks,
+                       const int32_t* docid, int rows, int mel, bf16* a, hipStream_t stream);
+
+// out[m, 0:dim] = bf16([sin(1000 t_m f), cos(1000 t_m f)]), f_i = exp(-i ln(1e4)/(dim/2-1))
+hipError_t timestep_sinusoid(const float* t, int n_t, int dim, bf16* out, hipStream_t stream);
+
+// x[r] += dt * ((1+cfg) v[r] - cfg v[r+rc]); x[r+rc] = x[r]   for r < rc
+hipError_t euler_cfg_update(float* x, const float* v, int rc, int mel, float dt, float cfg,
+                            hipStream_t stream);
+
+// [B, C, T] channel-first padded <-> packed rows [R, C]
+hipError_t pack_padded(const float* src, int batch, int channels, int padded_len,
+                       const int32_t* cu_seqlens, const int32_t* docid, const int32_t* pos,
+                       int rows, float* dst, hipStream_t stream);
+hipError_t unpack_padded(const float* src, int batch, int channels, int padded_len,
+                         const int32_t* cu_seqlens, float* dst, hipStream_t stream);
+
+}  // namespace fcv

@@ -1,0 +1,141 @@
+"""Packed CFG Euler solver over ``DiTEstimator`` (flashinfer_flow.py:16-74).
+
+``solve_euler_packed`` keeps the sample packed and fp32 across steps and runs the whole
+n-step loop inside libfcvdit (``fcv_dit_solve``), optionally captured once in a hipGraph.
+``solve_euler_batched`` keeps the reference's padded signature for callers that hand it
+``[B,80,T]`` tensors and a padding mask.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from typing import Any
+
+import torch
+
+from . import _lib
+from .estimator import DiTEstimator
+
+
+def euler_schedule(n_steps: int) -> tuple[list[float], list[float]]:
+    """Per-step (t, dt) of the cosine schedule with the reference's fp32 recurrence:
+    ``time = span[0]; dt = span[1]-span[0]``; after each step ``time += dt`` and
+    ``dt = span[step+1] - time`` (flashinfer_flow.py:34-43,71-73)."""
+    span = torch.linspace(0, 1, n_steps + 1, dtype=torch.float32)
+    span = 1 - torch.cos(span * 0.5 * torch.pi)
+    time = span[0]
+    dt = span[1] - span[0]
+    ts, dts = [], []
+    for step in range(1, n_steps + 1):
+        ts.append(float(time))
+        dts.append(float(dt))
+        time = time + dt
+        if step < n_steps:
+            dt = span[step + 1] - time
+    return ts, dts
+
+
+def _solver_buffers(estimator: DiTEstimator, rc: int, n_req: int) -> dict[str, torch.Tensor]:
+    """Packed CFG input buffers [2*rc, 80] (zero second halves) reused while the shape holds."""
+    key = (rc, n_req)
+    bufs = getattr(estimator, "_solver_bufs", None)
+    if bufs is None or bufs["key"] != key:
+        mel, dev = estimator.dims.mel_dim, estimator.device
+        z = lambda rows: torch.zeros(rows, mel, dtype=torch.float32, device=dev)
+        bufs = {"key": key, "x": z(2 * rc), "mu": z(2 * rc), "cond": z(2 * rc), "spks": z(2 * n_req)}
+        estimator._solver_bufs = bufs
+    return bufs
+
+
+def _stream_for(estimator: DiTEstimator) -> torch.cuda.Stream:
+    # hipGraph capture needs a non-default stream; default priority as required.
+    if estimator._stream is None:
+        estimator._stream = torch.cuda.Stream(device=estimator.device)
+    return estimator._stream
+
+
+@torch.no_grad()
+def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.Tensor,
+                       cond: torch.Tensor, spks: torch.Tensor, lengths: Sequence[int],
+                       n_steps: int = 10, cfg_rate: float = 0.7, streaming: bool = False,
+                       use_graph: bool = True) -> torch.Tensor:
+    """CFG Euler solve on packed request rows.
+
+    noise, mu, cond: ``[Rc, 80]`` conditional rows of the B requests (doc-major);
+    spks: ``[B, 80]``; lengths: the B request lengths.  The 2B-document CFG batch
+    ``[cond..., uncond...]`` (zero mu/cond/spks in the second half) is planned once and
+    the result ``[Rc, 80]`` fp32 is the sample after ``n_steps`` steps.
+    """
+    lengths = [int(n) for n in lengths]
+    rc = sum(lengths)
+    dev = estimator.device
+    f32 = lambda a: a.to(device=dev, dtype=torch.float32).contiguous()
+    noise, mu, cond, spks = f32(noise), f32(mu), f32(cond), f32(spks)
+    if noise.shape[0] != rc or mu.shape[0] != rc or cond.shape[0] != rc:
+        raise ValueError(f"noise, mu and cond must hold {rc} rows")
+    if spks.shape[0] != len(lengths):
+        raise ValueError("spks must hold one row per request")
+    ts, dts = euler_schedule(n_steps)
+    stream = _stream_for(estimator)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        estimator.plan(lengths + lengths, streaming)
+        # persistent solver buffers: stable pointers let a captured graph be replayed
+        buf = _solver_buffers(estimator, rc, len(lengths))
+        buf["x"][:rc].copy_(noise)
+        buf["x"][rc:].copy_(noise)
+        buf["mu"][:rc].copy_(mu)
+        buf["cond"][:rc].copy_(cond)
+        buf["spks"][: len(lengths)].copy_(spks)
+        t_arr = (_lib.c_float * n_steps)(*ts)
+        dt_arr = (_lib.c_float * n_steps)(*dts)
+        _lib.check(_lib.load().fcv_dit_solve(
+            estimator._require(), buf["x"].data_ptr(), buf["mu"].data_ptr(),
+            buf["cond"].data_ptr(), buf["spks"].data_ptr(), t_arr, dt_arr, n_steps,
+            float(cfg_rate), int(bool(use_graph)), stream.cuda_stream))
+        result = buf["x"][:rc].clone()
+    torch.cuda.current_stream(dev).wait_stream(stream)
+    return result
+
+
+@torch.no_grad()
+def solve_euler_batched(decoder: Any, noise: torch.Tensor, mu: torch.Tensor, mask: torch.Tensor,
+                        speaker_embeddings: torch.Tensor, condition: torch.Tensor,
+                        num_timesteps: int = 10, streaming: bool = False) -> torch.Tensor:
+    """Drop-in for the reference's ``solve_euler_batched`` (flashinfer_flow.py:16-74).
+
+    ``decoder.estimator`` must be a ``DiTEstimator``; ``decoder.inference_cfg_rate`` is the
+    CFG rate.  Padded ``[B,80,T]`` in, ``[B,80,T]`` out; padded frames keep the noise, as in
+    the reference (whose estimator returns zeros there).
+    """
+    estimator = decoder.estimator
+    if not isinstance(estimator, DiTEstimator):
+        raise TypeError("decoder.estimator must be a DiTEstimator")
+    lengths = [int(v) for v in mask[:, 0].sum(-1).round().to(torch.int64).tolist()]
+    batch, mel, _ = noise.shape
+    pack = lambda a: torch.cat([a[b, :, :n].transpose(0, 1) for b, n in enumerate(lengths)])
+    x = solve_euler_packed(estimator, pack(noise), pack(mu), pack(condition), speaker_embeddings,
+                           lengths, num_timesteps, float(decoder.inference_cfg_rate), streaming)
+    out = noise.to(device=x.device, dtype=torch.float32).clone()
+    off = 0
+    for b, n in enumerate(lengths):
+        out[b, :, :n] = x[off:off + n].transpose(0, 1)
+        off += n
+    return out.to(noise.dtype)
+
+
+def apply_mi355x(model: Any, device: torch.device | str = "cuda:0") -> DiTEstimator:
+    """Install ``DiTEstimator`` as ``model.flow.decoder.estimator`` (apply_flashinfer,
+    flashinfer_dit.py:951-988): same hyper-parameters as the estimator it replaces, its
+    state dict loaded (RoPE buffers excepted), weights finalized."""
+    old = model.flow.decoder.estimator
+    depth = len(old.transformer_blocks)
+    dim = old.proj_out.weight.shape[1]
+    heads = old.transformer_blocks[0].attn.heads if hasattr(old.transformer_blocks[0].attn, "heads") else 16
+    chunk = getattr(old, "static_chunk_size", 50)
+    new = DiTEstimator(dim=dim, depth=depth, heads=heads, dim_head=dim // heads,
+                       static_chunk_size=chunk, device=device)
+    new.load_reference_state_dict(old.state_dict())
+    new.finalize_weights()
+    model.flow.decoder.estimator = new
+    return new

@@ -1,0 +1,162 @@
+"""Write the golden vectors that pin the oracle's DiT wiring to the reference.
+
+Run in the build container only (the reference tree is not present on GPU hosts):
+
+    python tests/golden/make_golden.py [--ref /root/reference]
+
+It imports the reference's own ``cosyvoice/flow/DiT/dit.py``, ``modules.py``,
+``cosyvoice/utils/mask.py`` and ``flashinfer_flow.py`` (the module wiring of ``DiT.forward``,
+``dit.py:145-176``, and ``solve_euler_batched``, ``flashinfer_flow.py:16-74``, are not fixed by
+any closed form), feeds them seeded weights and inputs, and stores inputs + outputs as
+``.npz`` fixtures next to this script.  Two packages the reference imports are not installed
+here and are replaced by stubs registered in ``sys.modules`` before the import:
+
+* ``torchaudio`` -- used only by ``MelSpec`` (modules.py:24-65), never by the DiT; the stub is
+  an empty module;
+* ``x_transformers`` 2.23.5 -- ``RotaryEmbedding`` / ``apply_rotary_pos_emb``; the stub restates
+  the interleaved-pair rotation (the same arithmetic as the reference's Triton restatement,
+  flashinfer_kernels.py:219-249).  The fixtures therefore pin everything except the
+  x_transformers rotary arithmetic itself.
+"""
+
+from __future__ import annotations
+
+import argparse
+import sys
+import types
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+REPO = HERE.parent.parent
+
+
+def _install_stubs() -> None:
+    sys.modules.setdefault("torchaudio", types.ModuleType("torchaudio"))
+    xt = types.ModuleType("x_transformers")
+    xtx = types.ModuleType("x_transformers.x_transformers")
+
+    class RotaryEmbedding(torch.nn.Module):
+        def __init__(self, dim, base=10000.0):
+            super().__init__()
+            inv_freq = 1.0 / (base ** (torch.arange(0, dim, 2).float() / dim))
+            self.register_buffer("inv_freq", inv_freq)
+
+        def forward_from_seq_len(self, seq_len):
+            t = torch.arange(seq_len, device=self.inv_freq.device)
+            return self.forward(t)
+
+        def forward(self, t):
+            if t.ndim == 1:
+                t = t[None]
+            freqs = torch.einsum("bi,j->bij", t.type_as(self.inv_freq), self.inv_freq)
+            freqs = torch.stack((freqs, freqs), dim=-1).flatten(-2)
+            return freqs, 1.0
+
+    def _rotate_half(x):
+        x = x.reshape(*x.shape[:-1], x.shape[-1] // 2, 2)
+        x1, x2 = x.unbind(-1)
+        return torch.stack((-x2, x1), dim=-1).flatten(-2)
+
+    def apply_rotary_pos_emb(t, freqs, scale=1):
+        rot_dim, seq_len = freqs.shape[-1], t.shape[-2]
+        freqs = freqs[:, -seq_len:, :]
+        if t.ndim == 4 and freqs.ndim == 3:
+            freqs = freqs[:, None]
+        head, rest = t[..., :rot_dim], t[..., rot_dim:]
+        head = head * freqs.cos() * scale + _rotate_half(head) * freqs.sin() * scale
+        return torch.cat((head, rest), dim=-1).type(t.dtype)
+
+    xtx.RotaryEmbedding = RotaryEmbedding
+    xtx.apply_rotary_pos_emb = apply_rotary_pos_emb
+    xt.x_transformers = xtx
+    sys.modules.setdefault("x_transformers", xt)
+    sys.modules.setdefault("x_transformers.x_transformers", xtx)
+
+
+def _synthetic():
+    import importlib.util
+    name = "faster_cosyvoice_amd"
+    pkg_dir = REPO / "faster-cosyvoice_amd"
+    spec = importlib.util.spec_from_file_location(f"{name}_synthetic", pkg_dir / "synthetic.py")
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[spec.name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def _inputs(rng, B, T, lengths):
+    x = rng.standard_normal((B, 80, T)).astype(np.float32)
+    mu = rng.standard_normal((B, 80, T)).astype(np.float32)
+    cond = rng.standard_normal((B, 80, T)).astype(np.float32)
+    spks = rng.standard_normal((B, 80)).astype(np.float32)
+    t = rng.uniform(0, 1, size=(B,)).astype(np.float32)
+    mask = np.zeros((B, 1, T), np.float32)
+    for b, n in enumerate(lengths):
+        mask[b, 0, :n] = 1
+        cond[b, :, n:] = 0
+    return dict(x=x, mu=mu, cond=cond, spks=spks, t=t, mask=mask)
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--ref", default="/root/reference")
+    args = ap.parse_args()
+    _install_stubs()
+    sys.path.insert(0, args.ref)
+    from faster_cosyvoice.token2wav.cosyvoice.flow.DiT.dit import DiT  # noqa: E402
+    from faster_cosyvoice.token2wav.flashinfer_flow import solve_euler_batched  # noqa: E402
+
+    syn = _synthetic()
+    torch.set_grad_enabled(False)
+
+    # ---- tiny DiT: dim 128, depth 2, 2 heads x 64, padded batch of 2 ---------------------
+    dims = syn.DiTDims(dim=128, depth=2, heads=2, dim_head=64, ff_mult=2)
+    sd = syn.random_state_dict(dims, seed=11, gate_bias=0.5)
+    model = DiT(dim=128, depth=2, heads=2, dim_head=64, ff_mult=2, mel_dim=80, mu_dim=80,
+                spk_dim=80, out_channels=80, static_chunk_size=8, num_decoding_left_chunks=-1)
+    missing, unexpected = model.load_state_dict(sd, strict=False)
+    assert not unexpected and all("rotary" in k for k in missing), (missing, unexpected)
+    model.eval()
+    rng = np.random.Generator(np.random.PCG64(2024))
+    lengths = [40, 29]
+    inp = _inputs(rng, 2, 40, lengths)
+    tt = {k: torch.from_numpy(v) for k, v in inp.items()}
+    out_full = model(tt["x"], tt["mask"], tt["mu"], tt["t"], tt["spks"], tt["cond"], streaming=False)
+    out_stream = model(tt["x"], tt["mask"], tt["mu"], tt["t"], tt["spks"], tt["cond"], streaming=True)
+
+    decoder = types.SimpleNamespace(
+        inference_cfg_rate=0.7,
+        forward_estimator=lambda x, mask, mu, t, spks, cond, streaming: model(
+            x, mask, mu, t, spks, cond, streaming=streaming))
+    sample = solve_euler_batched(decoder, tt["x"], tt["mu"], tt["mask"], tt["spks"], tt["cond"],
+                                 num_timesteps=4, streaming=False)
+    np.savez_compressed(
+        HERE / "tiny_dit.npz", **inp, lengths=np.array(lengths, np.int32), chunk=np.int32(8),
+        weight_seed=np.int32(11), gate_bias=np.float32(0.5), dim=np.int32(128), depth=np.int32(2),
+        heads=np.int32(2), out_full=out_full.numpy(), out_stream=out_stream.numpy(),
+        euler_steps=np.int32(4), euler_cfg=np.float32(0.7), euler_sample=sample.float().numpy())
+
+    # ---- one full-size block: dim 1024, 16 heads, 64 frames, streaming chunk 50 ---------
+    dims = syn.DiTDims(dim=1024, depth=1)
+    sd = syn.random_state_dict(dims, seed=5, gate_bias=0.5)
+    model = DiT(dim=1024, depth=1, heads=16, dim_head=64, ff_mult=2, mel_dim=80, mu_dim=80,
+                spk_dim=80, out_channels=80, static_chunk_size=50, num_decoding_left_chunks=-1)
+    model.load_state_dict(sd, strict=False)
+    model.eval()
+    rng = np.random.Generator(np.random.PCG64(77))
+    inp = _inputs(rng, 1, 64, [64])
+    tt = {k: torch.from_numpy(v) for k, v in inp.items()}
+    out_full = model(tt["x"], tt["mask"], tt["mu"], tt["t"], tt["spks"], tt["cond"], streaming=False)
+    out_stream = model(tt["x"], tt["mask"], tt["mu"], tt["t"], tt["spks"], tt["cond"], streaming=True)
+    np.savez_compressed(
+        HERE / "block1024.npz", **inp, lengths=np.array([64], np.int32), chunk=np.int32(50),
+        weight_seed=np.int32(5), gate_bias=np.float32(0.5), dim=np.int32(1024), depth=np.int32(1),
+        heads=np.int32(16), out_full=out_full.numpy(), out_stream=out_stream.numpy())
+    print("wrote", sorted(p.name for p in HERE.glob("*.npz")))
+
+
+if __name__ == "__main__":
+    main()

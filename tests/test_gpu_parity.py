@@ -1,0 +1,222 @@
+"""GPU parity of the HIP estimator against the fp32 CPU oracle and the reference golden vectors.
+
+Tolerances: per-step velocity rel-L2 <= 1e-2 vs the fp32 path,
+mel rel-L2 <= 2e-2 after 10 Euler steps.  Where the oracle is given the same bf16-rounded
+weights the GPU uses, the remaining error is activation rounding only and the bound is tighter.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dit_oracle as O
+from tests.gpu_helpers import (bf16_weights, make_estimator, oracle_packed, random_packed, rel_l2,
+                               say)
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+VEL_TOL = 1e-2        # per-step velocity vs the fp32 reference path
+BF16_W_TOL = 5e-3     # vs the oracle running on the same bf16-rounded weights
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+@pytest.fixture(scope="module")
+def stress2(fcv):
+    """Two blocks at full width with AdaLN gates pushed to ~0.5 so every block matters."""
+    dims = fcv.synthetic.DiTDims(depth=2)
+    sd = fcv.synthetic.random_state_dict(dims, seed=21, gate_bias=0.5)
+    return sd, make_estimator(fcv, sd, depth=2)
+
+
+@pytest.fixture(scope="module")
+def full22(fcv):
+    say("[full22] drawing 22-layer weights")
+    sd = fcv.synthetic.random_state_dict(fcv.synthetic.DiTDims(), seed=0)
+    return sd, make_estimator(fcv, sd, depth=22)
+
+
+@pytest.mark.parametrize("streaming", [False, True])
+def test_one_block_300_frames(fcv, streaming):
+    """Workload 1 shape (one block, 300 frames) with nonzero gates."""
+    dims = fcv.synthetic.DiTDims(depth=1)
+    sd = fcv.synthetic.random_state_dict(dims, seed=1, gate_bias=0.5)
+    est = make_estimator(fcv, sd, depth=1)
+    x, mu, cond, spks, t = random_packed([300], seed=1)
+    say(f"[one_block] streaming={streaming}")
+    v = est.forward_packed(x, mu, cond, spks, t, [300], streaming=streaming).cpu()
+    ref32 = oracle_packed(sd, x, mu, cond, spks, t, [300], streaming)
+    ref16 = oracle_packed(bf16_weights(sd), x, mu, cond, spks, t, [300], streaming)
+    e32, e16 = rel_l2(v, ref32), rel_l2(v, ref16)
+    say(f"[one_block] rel_l2 vs fp32 {e32:.2e}, vs bf16-weight oracle {e16:.2e}")
+    assert e32 <= VEL_TOL and e16 <= BF16_W_TOL
+
+
+@pytest.mark.parametrize("streaming", [False, True])
+def test_reference_golden_block(fcv, streaming):
+    """GPU forward on the reference DiT's own outputs (tests/golden/block1024.npz)."""
+    g = dict(np.load(GOLDEN / "block1024.npz", allow_pickle=False))
+    dims = fcv.synthetic.DiTDims(depth=1)
+    sd = fcv.synthetic.random_state_dict(dims, seed=int(g["weight_seed"]),
+                                         gate_bias=float(g["gate_bias"]))
+    est = make_estimator(fcv, sd, depth=1, static_chunk_size=int(g["chunk"]))
+    dev = "cuda:0"
+    args = [torch.from_numpy(g[k]).to(dev) for k in ("x", "mask", "mu", "t", "spks", "cond")]
+    out = est(*args, streaming=streaming).cpu()
+    ref = torch.from_numpy(g["out_stream" if streaming else "out_full"])
+    err = rel_l2(out, ref)
+    say(f"[golden_block] streaming={streaming} rel_l2 {err:.2e}")
+    assert err <= VEL_TOL
+
+
+@pytest.mark.parametrize("streaming", [False, True])
+def test_ragged_docs_two_blocks(fcv, stress2, streaming):
+    """Ragged packing edge cases: a 1-frame doc, a doc of exactly one 128-row tile, docs that
+    straddle tiles, chunk boundaries not aligned to tiles."""
+    sd, est = stress2
+    lengths = [37, 128, 1, 200, 75]
+    x, mu, cond, spks, t = random_packed(lengths, seed=2)
+    v = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming).cpu()
+    ref = oracle_packed(bf16_weights(sd), x, mu, cond, spks, t, lengths, streaming)
+    off = 0
+    for n in lengths:
+        e = rel_l2(v[off:off + n], ref[off:off + n])
+        say(f"[ragged] streaming={streaming} len={n} rel_l2 {e:.2e}")
+        assert e <= BF16_W_TOL
+        off += n
+
+
+def test_shared_t_equals_per_doc_t(fcv, stress2):
+    sd, est = stress2
+    lengths = [50, 70]
+    x, mu, cond, spks, _ = random_packed(lengths, seed=3)
+    a = est.forward_packed(x, mu, cond, spks, torch.tensor([0.3]), lengths)
+    b = est.forward_packed(x, mu, cond, spks, torch.tensor([0.3, 0.3]), lengths)
+    assert torch.equal(a, b)
+
+
+def test_padded_dropin_matches_packed(fcv, stress2):
+    sd, est = stress2
+    lengths, T = [64, 33, 50], 64
+    x, mu, cond, spks, t = random_packed(lengths, seed=4)
+    pad = lambda rows: O.unpack(rows, lengths, T)
+    mask = torch.zeros(3, 1, T)
+    for b, n in enumerate(lengths):
+        mask[b, 0, :n] = 1
+    dev = "cuda:0"
+    out = est(pad(x).to(dev), mask.to(dev), pad(mu).to(dev), t.to(dev), spks.to(dev),
+              pad(cond).to(dev)).cpu()
+    packed = est.forward_packed(x, mu, cond, spks, t, lengths).cpu()
+    assert torch.equal(O.pack(out, lengths), packed)
+    for b, n in enumerate(lengths):
+        assert torch.all(out[b, :, n:] == 0)
+
+
+def test_missing_inputs_raise(fcv, stress2):
+    _, est = stress2
+    x = torch.zeros(1, 80, 8, device="cuda:0")
+    with pytest.raises(ValueError, match="spks and cond are required"):
+        est(x, torch.ones(1, 1, 8, device="cuda:0"), x, torch.zeros(1, device="cuda:0"), None, x)
+
+
+def test_batch_invariance_and_determinism(fcv, stress2):
+    """A document's velocity does not depend on its neighbours (no split-KV, per-row GEMMs),
+    and repeated calls are bit-identical (reference tests/gpu/test_stream_batched.py,
+    test_stream_flashinfer.py:87-92)."""
+    sd, est = stress2
+    lengths = [90, 300, 17, 150]
+    x, mu, cond, spks, _ = random_packed(lengths, seed=5)
+    t = torch.tensor([0.42])
+    for streaming in (False, True):
+        full = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming)
+        again = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming)
+        assert torch.equal(full, again)
+        off = 0
+        for d, n in enumerate(lengths):
+            alone = est.forward_packed(x[off:off + n], mu[off:off + n], cond[off:off + n],
+                                       spks[d:d + 1], t, [n], streaming=streaming)
+            assert torch.equal(alone, full[off:off + n]), (streaming, d)
+            off += n
+
+
+def test_streaming_prefix_stability_gate_a(fcv, stress2):
+    """Reference Gate A (tests/gpu/test_flashinfer_streaming_estimator.py:58-89): with the
+    chunk-causal mask the first floor(160/50)*50 frames of T=160 and T=200 agree; with full
+    attention they do not."""
+    _, est = stress2
+    x, mu, cond, spks, t = random_packed([200], seed=6)
+    t = torch.tensor([0.6])
+
+    def run(T, streaming):
+        return est.forward_packed(x[:T], mu[:T], cond[:T], spks, t, [T], streaming=streaming).cpu()
+
+    stable = 150
+    d_stream = (run(160, True)[:stable] - run(200, True)[:stable]).abs().max().item()
+    d_off = (run(160, False)[:stable] - run(200, False)[:stable]).abs().max().item()
+    say(f"[gate_a] stream diff {d_stream:.2e} offline diff {d_off:.2e}")
+    assert d_stream <= 1e-3
+    assert d_off > 1e-3
+
+
+def test_full_depth_single_request(fcv, full22):
+    """Workload 2: 22 layers, one request of 550 frames (prompt 250) as its CFG pair."""
+    sd, est = full22
+    b = fcv.synthetic.workload(2)
+    inp = b.cfg_inputs()
+    t = torch.tensor([b.t])
+    say("[dit22] GPU forward")
+    v = est.forward_packed(inp["x"], inp["mu"], inp["cond"], inp["spks"], t, b.doc_lengths).cpu()
+    say("[dit22] oracle forward")
+    ref = oracle_packed(sd, inp["x"], inp["mu"], inp["cond"], inp["spks"], t, b.doc_lengths)
+    err = rel_l2(v, ref)
+    say(f"[dit22] velocity rel_l2 vs fp32 oracle {err:.2e}")
+    assert err <= VEL_TOL
+
+
+def test_euler_solve_small_batch(fcv, full22):
+    """10-step CFG Euler: per-step velocity (GPU estimator fed the oracle's trajectory) and the
+    final mel of the GPU solve (graph and eager) against the fp32 oracle solve."""
+    sd, est = full22
+    b = fcv.synthetic.make_batch("small", [90, 61], [30, 20], seed=9)
+    pad = b.padded()
+    steps = []
+
+    def oracle_est(x, mask, mu, t, spks, cond, streaming):
+        return O.dit_forward(sd, x, mask, mu, t, spks, cond, streaming=streaming)
+
+    def observe(step, velocity, sample):
+        steps.append((step, sample.clone(), velocity.clone()))
+
+    say("[euler] oracle solve")
+    ref = O.solve_euler_batched(oracle_est, pad["noise"], pad["mu"], pad["mask"], pad["spks"],
+                                pad["cond"], n_steps=10, cfg_rate=0.7, on_step=observe)
+    ts, _ = fcv.euler_schedule(10)
+    lengths = b.doc_lengths
+    worst = 0.0
+    for step, sample, velocity in steps:
+        x_rows = torch.cat([O.pack(sample, b.lengths)] * 2)
+        zeros = torch.zeros_like(b.mu)
+        v = est.forward_packed(x_rows, torch.cat([b.mu, zeros]), torch.cat([b.cond, zeros]),
+                               torch.cat([b.spks, torch.zeros_like(b.spks)]),
+                               torch.tensor([ts[step - 1]]), lengths).cpu()
+        vref = torch.cat([O.pack(velocity[:2], b.lengths), O.pack(velocity[2:], b.lengths)])
+        worst = max(worst, rel_l2(v, vref))
+    say(f"[euler] worst per-step velocity rel_l2 {worst:.2e}")
+    assert worst <= VEL_TOL
+    ref_rows = O.pack(ref, b.lengths)
+    graph = fcv.solve_euler_packed(est, b.noise, b.mu, b.cond, b.spks, b.lengths, use_graph=True).cpu()
+    eager = fcv.solve_euler_packed(est, b.noise, b.mu, b.cond, b.spks, b.lengths, use_graph=False).cpu()
+    replay = fcv.solve_euler_packed(est, b.noise, b.mu, b.cond, b.spks, b.lengths, use_graph=True).cpu()
+    err = rel_l2(graph, ref_rows)
+    say(f"[euler] mel rel_l2 after 10 steps {err:.2e}")
+    assert err <= 2e-2
+    assert torch.equal(graph, eager) and torch.equal(graph, replay)
