@@ -5,7 +5,7 @@ parity test runs on seeded random-init weights with the reference DiT's
 state-dict layout (``cosyvoice/flow/DiT/dit.py:104-143``, hyper-parameters from
 ``builders.py:17-21``) and on seeded synthetic inputs.
 
-Draws use numpy's PCG64 ``Generator`` (float64 normal draws cast to float32),
+Draws use numpy's PCG64 ``Generator`` (float32 normal draws),
 which is platform independent, so the same seed gives the same tensors on any
 host.  Defaults: weights from seed 0, tensors from seed 1234, layouts from
 seed 0.
@@ -99,7 +99,7 @@ def random_state_dict(dims: DiTDims = DiTDims(), seed: int = 0, std: float = 0.0
     rng = np.random.Generator(np.random.PCG64(seed))
     sd = {}
     for name, shape in state_dict_shapes(dims):
-        arr = rng.standard_normal(int(np.prod(shape))).astype(np.float32) * np.float32(std)
+        arr = rng.standard_normal(int(np.prod(shape)), dtype=np.float32) * np.float32(std)
         sd[name] = torch.from_numpy(arr.reshape(shape))
     if gate_bias:
         for i in range(dims.depth):
@@ -175,7 +175,7 @@ class PackedBatch:
 
 
 def _normal(rng: np.random.Generator, *shape: int) -> torch.Tensor:
-    return torch.from_numpy(rng.standard_normal(int(np.prod(shape))).astype(np.float32).reshape(shape))
+    return torch.from_numpy(rng.standard_normal(int(np.prod(shape)), dtype=np.float32).reshape(shape))
 
 
 def make_batch(name: str, lengths: list[int], prompt_lengths: list[int], seed: int = 1234,
