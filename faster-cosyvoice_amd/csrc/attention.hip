@@ -9,10 +9,12 @@
 //
 // K/V tiles of 64 keys go through LDS double buffers: K row-major [key][dim] and V already
 // transposed [dim][key] (the QKV epilogue writes V transposed), both padded to 72 columns.
-// The first key tile starts at the document start rounded down to 8 keys so every 16-byte
-// V^T load is aligned; keys outside [doc start, kv_end) and, in chunk mode, keys in a later
-// chunk than the query are masked to -inf.  No split-KV: each (query, head) is reduced by
-// exactly one wave in key order, so results do not depend on the batch composition.
+// Documents start at 8-row aligned rows of the internal layout, so every 16-byte V^T load is
+// aligned and key tiles always start at the document start: a document's key partition, and
+// hence its fp32 rounding, is the same wherever it sits in the batch.  Keys at or past kv_end
+// and, in chunk mode, keys in a later chunk than the query are masked to -inf.  No split-KV:
+// each (query, head) is reduced by exactly one wave in key order, so results do not depend on
+// the batch composition.
 #include "kernels.hpp"
 
 namespace fcv {
@@ -25,8 +27,8 @@ constexpr int LDP = 72;         // padded LDS row (bf16 elements)
 
 __global__ __launch_bounds__(256, 2) void attention_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ VT,
-    bf16* __restrict__ O, const int32_t* __restrict__ cu, const int32_t* __restrict__ tiles,
-    int rows, int rp, int heads, int chunk, float scale_log2) {
+    bf16* __restrict__ O, const int32_t* __restrict__ dstart, const int32_t* __restrict__ dlen,
+    const int32_t* __restrict__ tiles, int rows, int rp, int heads, int chunk, float scale_log2) {
   __shared__ __attribute__((aligned(16))) bf16 sK[2][TK][LDP];
   __shared__ __attribute__((aligned(16))) bf16 sV[2][HD][LDP];
 
@@ -34,15 +36,15 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
   const int head = blockIdx.x % heads;
   const int doc = tiles[2 * tile];
   const int q0 = tiles[2 * tile + 1];
-  const int doc_start = cu[doc];
-  const int doc_end = cu[doc + 1];
+  const int doc_start = dstart[doc];
+  const int doc_end = doc_start + dlen[doc];
   const int q_last = min(q0 + TQ - 1, doc_end - 1);
   int kv_end = doc_end;
   if (chunk > 0) {
     int lim = ((q_last - doc_start) / chunk + 1) * chunk;
     kv_end = min(doc_end, doc_start + lim);
   }
-  const int kv_begin = doc_start & ~7;
+  const int kv_begin = doc_start;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int key = kb + kt * 32 + (e >> 2) * 8 + hl * 4 + (e & 3);
-        const bool ok = key >= doc_start && key < key_lim;
+        const bool ok = key < key_lim;
         float v = ok ? s[kt][e] * scale_log2 : -INFINITY;
         s[kt][e] = v;
         tmax = fmaxf(tmax, v);
@@ -202,12 +204,13 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
 }  // namespace
 
 hipError_t attention_varlen(const bf16* q, const bf16* k, const bf16* vt, bf16* o,
-                            const int32_t* cu_seqlens, const int32_t* tiles, int n_tiles,
-                            int rows, int rp, int heads, int chunk, hipStream_t stream) {
+                            const int32_t* doc_start, const int32_t* doc_len,
+                            const int32_t* tiles, int n_tiles, int rows, int rp, int heads,
+                            int chunk, hipStream_t stream) {
   if (n_tiles <= 0) return hipSuccess;
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // 64^-0.5 * log2(e)
   hipLaunchKernelGGL(attention_kernel, dim3(n_tiles * heads), dim3(256), 0, stream, q, k, vt, o,
-                     cu_seqlens, tiles, rows, rp, heads, chunk, scale_log2);
+                     doc_start, doc_len, tiles, rows, rp, heads, chunk, scale_log2);
   return hipGetLastError();
 }
 

@@ -39,14 +39,22 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct Layout {
   // byte offsets inside the workspace
-  size_t h, nbuf, obuf, q, k, vt, u, ain, vbuf, docid, pos, cu, tiles, mod, tsin, t1, t2, tbuf;
+  size_t h, nbuf, obuf, q, k, vt, u, ain, vbuf;
+  size_t docid, pos, ext_row, docid_ext, pos_ext, cu_int, lens, cu_ext, tiles;
+  size_t mod, tsin, t1, t2, tbuf;
   size_t total;
 };
 
+// Internal rows: every document starts at a multiple of 8 rows (at most 7 pad rows each), so
+// attention key tiles and 16-byte V^T loads are aligned to the document start.
+long internal_rows_bound(long rows, long n_docs) { return rows + 7 * n_docs; }
+
 Layout make_layout(const FcvDitDims& d, long rows, long n_docs) {
-  const long rp = align_up(std::max<long>(rows, 1), kRowTile);
-  const long n_tiles = rows / fcv::kAttnTileQ + n_docs + 1;
+  const long ri = internal_rows_bound(rows, n_docs);
+  const long rp = align_up(std::max<long>(ri, 1), kRowTile);
+  const long n_tiles = ri / fcv::kAttnTileQ + n_docs + 1;
   const long mod_width = (long)d.depth * 6 * d.dim + 2L * d.dim;
+  const long nd = std::max<long>(n_docs, 1);
   Layout L{};
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -62,15 +70,20 @@ Layout make_layout(const FcvDitDims& d, long rows, long n_docs) {
   L.vt = take(rp * d.dim * 2);
   L.u = take(rp * (long)d.ff_dim * 2);
   L.ain = take(rp * 4L * d.mel_dim * 2);
-  L.vbuf = take(rp * (long)d.mel_dim * 4);
+  L.vbuf = take(std::max<long>(rows, 1) * (long)d.mel_dim * 4);
   L.docid = take(rp * 4);
   L.pos = take(rp * 4);
-  L.cu = take((n_docs + 1) * 4);
+  L.ext_row = take(rp * 4);
+  L.docid_ext = take(std::max<long>(rows, 1) * 4);
+  L.pos_ext = take(std::max<long>(rows, 1) * 4);
+  L.cu_int = take((nd + 1) * 4);
+  L.lens = take(nd * 4);
+  L.cu_ext = take((nd + 1) * 4);
   L.tiles = take(n_tiles * 2 * 4);
-  L.mod = take(std::max<long>(n_docs, 1) * mod_width * 4);
-  L.tsin = take(std::max<long>(n_docs, 1) * 256 * 2);
-  L.t1 = take(std::max<long>(n_docs, 1) * (long)d.dim * 2);
-  L.t2 = take(std::max<long>(n_docs, 1) * (long)d.dim * 2);
+  L.mod = take(nd * mod_width * 4);
+  L.tsin = take(nd * 256 * 2);
+  L.t1 = take(nd * (long)d.dim * 2);
+  L.t2 = take(nd * (long)d.dim * 2);
   L.tbuf = take(kMaxSteps * 4);
   L.total = off;
   return L;
@@ -83,10 +96,10 @@ struct FcvDit {
   FcvDitWeights w{};
   long mod_width = 0;
 
-  // plan
+  // plan: `rows` caller rows (cu_host); `rows_int` internal 8-aligned rows, rp >= rows_int
   bool planned = false;
   unsigned long generation = 0;
-  int rows = 0, rp = 0, n_docs = 0, n_tiles = 0, mask_mode = 0, chunk = 0;
+  int rows = 0, rows_int = 0, rp = 0, n_docs = 0, n_tiles = 0, mask_mode = 0, chunk = 0;
   std::vector<int32_t> cu_host;
   char* ws = nullptr;
   size_t ws_bytes = 0;
@@ -113,7 +126,7 @@ int run_forward(FcvDit* m, const float* x, const float* mu, const float* cond, c
                 const float* t, int n_t, float* v_out, hipStream_t s) {
   const FcvDitDims& d = m->dims;
   const FcvDitWeights& w = m->w;
-  const int R = m->rows, D = d.dim, F = d.ff_dim, mel = d.mel_dim;
+  const int R = m->rows_int, D = d.dim, F = d.ff_dim, mel = d.mel_dim;
   const long mod_stride = (n_t == 1) ? 0 : m->mod_width;
   auto B = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
 
@@ -127,7 +140,9 @@ int run_forward(FcvDit* m, const float* x, const float* mu, const float* cond, c
   bf16* ain = m->at<bf16>(m->L.ain);
   int32_t* docid = m->at<int32_t>(m->L.docid);
   int32_t* pos = m->at<int32_t>(m->L.pos);
-  int32_t* cu = m->at<int32_t>(m->L.cu);
+  int32_t* ext_row = m->at<int32_t>(m->L.ext_row);
+  int32_t* cu_int = m->at<int32_t>(m->L.cu_int);
+  int32_t* lens = m->at<int32_t>(m->L.lens);
   int32_t* tiles = m->at<int32_t>(m->L.tiles);
   float* mod = m->at<float>(m->L.mod);
   bf16* tsin = m->at<bf16>(m->L.tsin);
@@ -143,7 +158,7 @@ int run_forward(FcvDit* m, const float* x, const float* mu, const float* cond, c
                              (int)m->mod_width, (int)m->mod_width, s));
 
   // input projection + causal conv position embedding (InputEmbedding dit.py:84-98)
-  FCV_HIP(fcv::pack_inputs(x, cond, mu, spks, docid, R, mel, ain, s));
+  FCV_HIP(fcv::pack_inputs(x, cond, mu, spks, docid, ext_row, R, mel, ain, s));
   FCV_HIP(fcv::gemm_bias_f32_bf16(ain, 4 * mel, B(w.in_w), 4 * mel, w.in_b, R, D, 4 * mel, h,
                                   nbuf, D, s));
   FCV_HIP(fcv::conv_causal_mish(nbuf, D, B(w.conv1_w), w.conv1_b, d.conv_kernel, pos, R, obuf,
@@ -158,9 +173,10 @@ int run_forward(FcvDit* m, const float* x, const float* mu, const float* cond, c
                                      docid, nbuf, s));
     FCV_HIP(fcv::gemm_qkv_rope(nbuf, D, B(w.qkv_w) + (long)l * 3 * D * D, D,
                                w.qkv_b + (long)l * 3 * D, R, D, d.heads, pos, w.rope_cos,
-                               w.rope_sin, d.rope_dim, q, k, vt, m->rp, s));
-    FCV_HIP(fcv::attention_varlen(q, k, vt, obuf, cu, tiles, m->n_tiles, R, m->rp, d.heads,
-                                  m->mask_mode == FCV_MASK_CHUNK_CAUSAL ? m->chunk : 0, s));
+                               w.rope_sin, d.rope_dim, d.max_pos, q, k, vt, m->rp, s));
+    FCV_HIP(fcv::attention_varlen(q, k, vt, obuf, cu_int, lens, tiles, m->n_tiles, R, m->rp,
+                                  d.heads, m->mask_mode == FCV_MASK_CHUNK_CAUSAL ? m->chunk : 0,
+                                  s));
     FCV_HIP(fcv::gemm_gated_residual(obuf, D, B(w.out_w) + (long)l * D * D, D,
                                      w.out_b + (long)l * D, R, D, D, h, D, mod + base + 2 * D,
                                      mod_stride, docid, s));
@@ -177,7 +193,8 @@ int run_forward(FcvDit* m, const float* x, const float* mu, const float* cond, c
   const long fin = (long)d.depth * 6 * D;
   FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(fin + D), (int)fin, docid,
                                    nbuf, s));
-  FCV_HIP(fcv::gemm_bias_f32(nbuf, D, B(w.proj_w), D, w.proj_b, R, 128, D, v_out, mel, mel, s));
+  FCV_HIP(fcv::gemm_bias_f32_rowmap(nbuf, D, B(w.proj_w), D, w.proj_b, R, 128, D, v_out, mel,
+                                    mel, ext_row, s));
   return FCV_OK;
 }
 
@@ -247,11 +264,19 @@ int fcv_dit_plan(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask
   const int rows = cu_host[n_docs];
   FCV_CHECK(rows <= (1 << 24), FCV_ERR_INVALID, "too many rows");
 
-  // attention tiles: (doc, first query row), most expensive first (LPT order)
+  // internal layout: document starts rounded up to multiples of 8 rows
+  std::vector<int32_t> cu_int(n_docs + 1, 0), lens(n_docs);
+  for (int d = 0; d < n_docs; ++d) {
+    lens[d] = cu_host[d + 1] - cu_host[d];
+    cu_int[d + 1] = cu_int[d] + (int32_t)align_up(lens[d], 8);
+  }
+  const int rows_int = cu_int[n_docs];
+
+  // attention tiles: (doc, first internal query row), most expensive first (LPT order)
   struct T { int doc, q0; long cost; };
   std::vector<T> tl;
   for (int d = 0; d < n_docs; ++d) {
-    const int start = cu_host[d], end = cu_host[d + 1];
+    const int start = cu_int[d], end = cu_int[d] + lens[d];
     for (int q0 = start; q0 < end; q0 += fcv::kAttnTileQ) {
       int q_last = std::min(q0 + fcv::kAttnTileQ - 1, end - 1);
       long kv = end - start;
@@ -282,19 +307,28 @@ int fcv_dit_plan(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask
   m->ws_bytes = workspace_bytes;
   m->L = L;
   m->rows = rows;
-  m->rp = (int)align_up(std::max(rows, 1), kRowTile);
+  m->rows_int = rows_int;
+  m->rp = (int)align_up(std::max(rows_int, 1), kRowTile);
   m->n_docs = n_docs;
   m->n_tiles = (int)tl.size();
   m->mask_mode = mask_mode;
   m->chunk = mask_mode == FCV_MASK_CHUNK_CAUSAL ? chunk : 0;
   m->cu_host.assign(cu_host, cu_host + n_docs + 1);
 
-  FCV_HIP(hipMemcpyAsync(m->at<int32_t>(L.cu), cu_host, (n_docs + 1) * sizeof(int32_t),
-                         hipMemcpyHostToDevice, s));
-  FCV_HIP(hipMemcpyAsync(m->at<int32_t>(L.tiles), tiles_host.data(),
-                         tiles_host.size() * sizeof(int32_t), hipMemcpyHostToDevice, s));
-  FCV_HIP(fcv::build_row_index(m->at<int32_t>(L.cu), n_docs, rows, m->at<int32_t>(L.docid),
-                               m->at<int32_t>(L.pos), s));
+  auto h2d = [&](size_t off, const std::vector<int32_t>& v) {
+    return hipMemcpyAsync(m->ws + off, v.data(), v.size() * sizeof(int32_t),
+                          hipMemcpyHostToDevice, s);
+  };
+  FCV_HIP(h2d(L.cu_ext, m->cu_host));
+  FCV_HIP(h2d(L.cu_int, cu_int));
+  FCV_HIP(h2d(L.lens, lens));
+  FCV_HIP(h2d(L.tiles, tiles_host));
+  FCV_HIP(fcv::build_row_index(m->at<int32_t>(L.cu_ext), n_docs, rows,
+                               m->at<int32_t>(L.docid_ext), m->at<int32_t>(L.pos_ext), s));
+  FCV_HIP(fcv::build_aligned_row_index(m->at<int32_t>(L.cu_int), m->at<int32_t>(L.lens),
+                                       m->at<int32_t>(L.cu_ext), n_docs, rows_int,
+                                       m->at<int32_t>(L.docid), m->at<int32_t>(L.pos),
+                                       m->at<int32_t>(L.ext_row), s));
   FCV_HIP(hipStreamSynchronize(s));
   m->planned = true;
   m->generation++;
@@ -406,8 +440,9 @@ int fcv_pack_padded(FcvDit* m, const float* src, int32_t batch, int32_t channels
   for (int d = 0; d < m->n_docs; ++d)
     FCV_CHECK(m->cu_host[d + 1] - m->cu_host[d] <= padded_len, FCV_ERR_INVALID,
               "document longer than padded_len");
-  FCV_HIP(fcv::pack_padded(src, batch, channels, padded_len, m->at<int32_t>(m->L.cu),
-                           m->at<int32_t>(m->L.docid), m->at<int32_t>(m->L.pos), m->rows, dst, s));
+  FCV_HIP(fcv::pack_padded(src, batch, channels, padded_len, m->at<int32_t>(m->L.cu_ext),
+                           m->at<int32_t>(m->L.docid_ext), m->at<int32_t>(m->L.pos_ext), m->rows,
+                           dst, s));
   return FCV_OK;
 }
 
@@ -419,7 +454,8 @@ int fcv_unpack_padded(FcvDit* m, const float* src, int32_t batch, int32_t channe
   for (int d = 0; d < m->n_docs; ++d)
     FCV_CHECK(m->cu_host[d + 1] - m->cu_host[d] <= padded_len, FCV_ERR_INVALID,
               "document longer than padded_len");
-  FCV_HIP(fcv::unpack_padded(src, batch, channels, padded_len, m->at<int32_t>(m->L.cu), dst, s));
+  FCV_HIP(fcv::unpack_padded(src, batch, channels, padded_len, m->at<int32_t>(m->L.cu_ext), dst,
+                             s));
   return FCV_OK;
 }
 

@@ -63,10 +63,30 @@ __global__ void row_index_kernel(const int32_t* __restrict__ cu, int n_docs, int
   pos[r] = r - cu[lo];
 }
 
+__global__ void aligned_row_index_kernel(const int32_t* __restrict__ cu_int,
+                                         const int32_t* __restrict__ lens,
+                                         const int32_t* __restrict__ cu_ext, int n_docs,
+                                         int rows_int, int32_t* __restrict__ docid,
+                                         int32_t* __restrict__ pos,
+                                         int32_t* __restrict__ ext_row) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows_int) return;
+  int lo = 0, hi = n_docs - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (cu_int[mid] <= r) lo = mid; else hi = mid - 1;
+  }
+  const int p = r - cu_int[lo];
+  docid[r] = lo;
+  pos[r] = p;
+  ext_row[r] = p < lens[lo] ? cu_ext[lo] + p : -1;
+}
+
 // one thread per 8 output columns
 __global__ void pack_inputs_kernel(const float* __restrict__ x, const float* __restrict__ cond,
                                    const float* __restrict__ mu, const float* __restrict__ spks,
-                                   const int32_t* __restrict__ docid, int rows, int mel,
+                                   const int32_t* __restrict__ docid,
+                                   const int32_t* __restrict__ ext_row, int rows, int mel,
                                    bf16* __restrict__ a) {
   const int per_row = (4 * mel) / 8;
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -74,14 +94,18 @@ __global__ void pack_inputs_kernel(const float* __restrict__ x, const float* __r
   const int r = (int)(idx / per_row);
   const int c = (int)(idx % per_row) * 8;
   const int seg = c / mel, off = c % mel;
-  const float* src;
-  if (seg == 0) src = x + (long)r * mel;
-  else if (seg == 1) src = cond + (long)r * mel;
-  else if (seg == 2) src = mu + (long)r * mel;
-  else src = spks + (long)docid[r] * mel;
-  const float4 u = *reinterpret_cast<const float4*>(src + off);
-  const float4 w = *reinterpret_cast<const float4*>(src + off + 4);
-  bf16x8 o = {f2bf(u.x), f2bf(u.y), f2bf(u.z), f2bf(u.w), f2bf(w.x), f2bf(w.y), f2bf(w.z), f2bf(w.w)};
+  const int e = ext_row[r];
+  bf16x8 o = {};
+  if (e >= 0) {
+    const float* src;
+    if (seg == 0) src = x + (long)e * mel;
+    else if (seg == 1) src = cond + (long)e * mel;
+    else if (seg == 2) src = mu + (long)e * mel;
+    else src = spks + (long)docid[r] * mel;
+    const float4 u = *reinterpret_cast<const float4*>(src + off);
+    const float4 w = *reinterpret_cast<const float4*>(src + off + 4);
+    o = bf16x8{f2bf(u.x), f2bf(u.y), f2bf(u.z), f2bf(u.w), f2bf(w.x), f2bf(w.y), f2bf(w.z), f2bf(w.w)};
+  }
   *reinterpret_cast<bf16x8*>(a + (long)r * 4 * mel + c) = o;
 }
 
@@ -156,13 +180,23 @@ hipError_t build_row_index(const int32_t* cu_seqlens, int n_docs, int rows, int3
   return hipGetLastError();
 }
 
+hipError_t build_aligned_row_index(const int32_t* cu_int, const int32_t* lens,
+                                   const int32_t* cu_ext, int n_docs, int rows_int, int32_t* docid,
+                                   int32_t* pos, int32_t* ext_row, hipStream_t stream) {
+  if (rows_int <= 0) return hipSuccess;
+  hipLaunchKernelGGL(aligned_row_index_kernel, dim3(blocks_for(rows_int, 256)), dim3(256), 0,
+                     stream, cu_int, lens, cu_ext, n_docs, rows_int, docid, pos, ext_row);
+  return hipGetLastError();
+}
+
 hipError_t pack_inputs(const float* x, const float* cond, const float* mu, const float* spks,
-                       const int32_t* docid, int rows, int mel, bf16* a, hipStream_t stream) {
+                       const int32_t* docid, const int32_t* ext_row, int rows, int mel, bf16* a,
+                       hipStream_t stream) {
   if (rows <= 0) return hipSuccess;
   if (mel % 8 != 0) return hipErrorInvalidValue;
   const long n = (long)rows * (4 * mel / 8);
   hipLaunchKernelGGL(pack_inputs_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, x, cond,
-                     mu, spks, docid, rows, mel, a);
+                     mu, spks, docid, ext_row, rows, mel, a);
   return hipGetLastError();
 }
 

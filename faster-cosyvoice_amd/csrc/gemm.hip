@@ -153,6 +153,26 @@ struct EpiBiasF32 {
   }
 };
 
+struct EpiBiasF32RowMap {
+  const float* bias;
+  float* out;
+  int ldo;
+  int n_valid;
+  const int32_t* row_map;
+  __device__ void operator()(const f32x4& v, int row0, int col, int M) const {
+    if (col >= n_valid) return;
+    const float b = bias[col];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int row = row0 + r;
+      if (row < M) {
+        int dst = row_map[row];
+        if (dst >= 0) out[(long)dst * ldo + col] = v[r] + b;
+      }
+    }
+  }
+};
+
 struct EpiBiasSiluBf16 {
   const float* bias;
   bf16* out;
@@ -210,6 +230,7 @@ struct EpiQkvRope {
   const float* rope_cos;
   const float* rope_sin;
   int rope_dim;
+  int max_pos;
   bf16* q;
   bf16* k;
   bf16* vt;
@@ -232,7 +253,7 @@ struct EpiQkvRope {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         int row = min(row0 + r, M - 1);
-        int p = pos[row];
+        int p = min(pos[row], max_pos - 1);  // pad rows run past the document
         float cs = rope_cos[p * half + (c >> 1)];
         float sn = rope_sin[p * half + (c >> 1)];
         y[r] = y[r] * cs + sign * partner[r] * sn;
@@ -277,6 +298,13 @@ hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const f
   return launch(A, lda, W, ldw, M, N, K, EpiBiasF32{bias, out, ldo, n_valid}, stream);
 }
 
+hipError_t gemm_bias_f32_rowmap(const bf16* A, int lda, const bf16* W, int ldw,
+                                const float* bias, int M, int N, int K, float* out, int ldo,
+                                int n_valid, const int32_t* row_map, hipStream_t stream) {
+  return launch(A, lda, W, ldw, M, N, K, EpiBiasF32RowMap{bias, out, ldo, n_valid, row_map},
+                stream);
+}
+
 hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, bf16* out, int ldo, hipStream_t stream) {
   return launch(A, lda, W, ldw, M, N, K, EpiBiasSiluBf16{bias, out, ldo}, stream);
@@ -296,11 +324,11 @@ hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, c
 
 hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const float* bias, int M,
                          int dim, int heads, const int32_t* pos, const float* rope_cos,
-                         const float* rope_sin, int rope_dim, bf16* q, bf16* k, bf16* vt, int rp,
-                         hipStream_t stream) {
+                         const float* rope_sin, int rope_dim, int max_pos, bf16* q, bf16* k,
+                         bf16* vt, int rp, hipStream_t stream) {
   (void)heads;
   return launch(A, lda, W, ldw, M, 3 * dim, dim,
-                EpiQkvRope{bias, dim, M, pos, rope_cos, rope_sin, rope_dim, q, k, vt, rp},
+                EpiQkvRope{bias, dim, M, pos, rope_cos, rope_sin, rope_dim, max_pos, q, k, vt, rp},
                 stream);
 }
 

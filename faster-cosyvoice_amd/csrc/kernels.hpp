@@ -17,9 +17,14 @@ hipError_t gemm_bias_f32_bf16(const bf16* A, int lda, const bf16* W, int ldw, co
                               int M, int N, int K, float* out_f32, bf16* out_bf16, int ldo,
                               hipStream_t stream);
 
-// out[r, c] = acc + bias[c] for c < n_valid (fp32; proj_out, AdaLN projection)
+// out[r, c] = acc + bias[c] for c < n_valid (fp32; AdaLN projection)
 hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                          int M, int N, int K, float* out, int ldo, int n_valid, hipStream_t stream);
+
+// out[row_map[r], c] = acc + bias[c] for c < n_valid and row_map[r] >= 0 (proj_out)
+hipError_t gemm_bias_f32_rowmap(const bf16* A, int lda, const bf16* W, int ldw,
+                                const float* bias, int M, int N, int K, float* out, int ldo,
+                                int n_valid, const int32_t* row_map, hipStream_t stream);
 
 // out[r, c] = bf16(silu(acc + bias[c]))   (timestep MLP)
 hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
@@ -36,20 +41,22 @@ hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, c
                                long mod_stride, const int32_t* docid, hipStream_t stream);
 
 // Fused QKV projection: bias, interleaved RoPE on columns [0, rope_dim) of q and k
-// (angles from cos/sin tables [max_pos][rope_dim/2], row position from pos[r]),
+// (angles from cos/sin tables [max_pos][rope_dim/2], row position min(pos[r], max_pos-1)),
 // scatter to q, k : [heads][M][dim_head] and vt : [heads][dim_head][rp] (V transposed).
 hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const float* bias, int M,
                          int dim, int heads, const int32_t* pos, const float* rope_cos,
-                         const float* rope_sin, int rope_dim, bf16* q, bf16* k, bf16* vt, int rp,
-                         hipStream_t stream);
+                         const float* rope_sin, int rope_dim, int max_pos, bf16* q, bf16* k,
+                         bf16* vt, int rp, hipStream_t stream);
 
 // ---- attention ----------------------------------------------------------------------------
-// Varlen attention over cu_seqlens, head_dim 64. tiles[i] = {doc, first query row}.
+// Varlen attention, head_dim 64.  Document d starts at row doc_start[d] (a multiple of 8)
+// and has doc_len[d] real rows; tiles[i] = {doc, first query row}.
 // chunk == 0: full attention inside each document; chunk > 0: key visible iff
 // (key_pos / chunk) <= (query_pos / chunk).
 hipError_t attention_varlen(const bf16* q, const bf16* k, const bf16* vt, bf16* o,
-                            const int32_t* cu_seqlens, const int32_t* tiles, int n_tiles, int rows,
-                            int rp, int heads, int chunk, hipStream_t stream);
+                            const int32_t* doc_start, const int32_t* doc_len,
+                            const int32_t* tiles, int n_tiles, int rows, int rp, int heads,
+                            int chunk, hipStream_t stream);
 constexpr int kAttnTileQ = 128;
 
 // ---- causal grouped conv position embedding (64 channels per group) -------------------------
@@ -69,9 +76,17 @@ hipError_t layer_norm_modulate(const float* h, int C, int rows, const float* mod
 hipError_t build_row_index(const int32_t* cu_seqlens, int n_docs, int rows, int32_t* docid,
                            int32_t* pos, hipStream_t stream);
 
-// a[r, 0:4*mel] = bf16([x[r], cond[r], mu[r], spks[docid[r]]])
+// Internal (8-row aligned) layout: document d owns internal rows [cu_int[d], cu_int[d+1]) of
+// which the first lens[d] are real.  docid/pos of every internal row; ext_row = caller row of
+// a real row, -1 for a pad row.
+hipError_t build_aligned_row_index(const int32_t* cu_int, const int32_t* lens,
+                                   const int32_t* cu_ext, int n_docs, int rows_int, int32_t* docid,
+                                   int32_t* pos, int32_t* ext_row, hipStream_t stream);
+
+// a[r, 0:4*mel] = bf16([x[e], cond[e], mu[e], spks[docid[r]]]) with e = ext_row[r]; zeros when e < 0
 hipError_t pack_inputs(const float* x, const float* cond, const float* mu, const float* spks,
-                       const int32_t* docid, int rows, int mel, bf16* a, hipStream_t stream);
+                       const int32_t* docid, const int32_t* ext_row, int rows, int mel, bf16* a,
+                       hipStream_t stream);
 
 // out[m, 0:dim] = bf16([sin(1000 t_m f), cos(1000 t_m f)]), f_i = exp(-i ln(1e4)/(dim/2-1))
 hipError_t timestep_sinusoid(const float* t, int n_t, int dim, bf16* out, hipStream_t stream);
