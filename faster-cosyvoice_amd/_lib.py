@@ -55,7 +55,12 @@ SIGNATURES = {
                                   c_void_p]),
     "fcv_unpack_padded": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p,
                                     c_void_p]),
+    "fcv_dit_probe_arm": (c_int32, [c_void_p, c_int32, c_int32]),
+    "fcv_dit_probe_read": (c_int32, [c_void_p, POINTER(c_float), c_int32, POINTER(c_int32)]),
 }
+
+STAGES = ("qkv", "attention", "out_proj", "ff1", "ff2", "ln_mod", "conv", "adaln", "in_proj",
+          "proj_out", "euler", "forward")
 
 _LIB: ctypes.CDLL | None = None
 

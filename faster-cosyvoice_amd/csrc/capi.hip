@@ -105,6 +105,12 @@ struct FcvDit {
   size_t ws_bytes = 0;
   Layout L{};
 
+  // timing probe (fcv_dit_probe_arm)
+  int probe_stage = -1;
+  int probe_pairs = 0;
+  int probe_count = 0;
+  std::vector<hipEvent_t> probe_events;
+
   // graph cache
   hipGraphExec_t graph_exec = nullptr;
   unsigned long graph_generation = 0;
@@ -118,12 +124,42 @@ struct FcvDit {
     graph_exec = nullptr;
     graph_key.clear();
   }
+
+  void drop_probe() {
+    for (hipEvent_t e : probe_events) (void)hipEventDestroy(e);
+    probe_events.clear();
+    probe_stage = -1;
+    probe_pairs = 0;
+    probe_count = 0;
+  }
+
+  // event pair around one launch of `stage` in block `layer` (-1 = outside the blocks)
+  hipError_t probe_begin(int stage, int layer, hipStream_t s) {
+    if (stage != probe_stage || layer > 0 || probe_count >= probe_pairs) return hipSuccess;
+    return hipEventRecord(probe_events[2 * probe_count], s);
+  }
+  hipError_t probe_end(int stage, int layer, hipStream_t s) {
+    if (stage != probe_stage || layer > 0 || probe_count >= probe_pairs) return hipSuccess;
+    return hipEventRecord(probe_events[2 * probe_count++ + 1], s);
+  }
 };
 
 namespace {
 
+int run_forward_body(FcvDit* m, const float* x, const float* mu, const float* cond,
+                     const float* spks, const float* t, int n_t, float* v_out, hipStream_t s);
+
 int run_forward(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
                 const float* t, int n_t, float* v_out, hipStream_t s) {
+  FCV_HIP(m->probe_begin(FCV_STAGE_FORWARD, -1, s));
+  int rc = run_forward_body(m, x, mu, cond, spks, t, n_t, v_out, s);
+  if (rc != FCV_OK) return rc;
+  FCV_HIP(m->probe_end(FCV_STAGE_FORWARD, -1, s));
+  return FCV_OK;
+}
+
+int run_forward_body(FcvDit* m, const float* x, const float* mu, const float* cond,
+                     const float* spks, const float* t, int n_t, float* v_out, hipStream_t s) {
   const FcvDitDims& d = m->dims;
   const FcvDitWeights& w = m->w;
   const int R = m->rows_int, D = d.dim, F = d.ff_dim, mel = d.mel_dim;
@@ -154,47 +190,67 @@ int run_forward(FcvDit* m, const float* x, const float* mu, const float* cond, c
   FCV_HIP(fcv::timestep_sinusoid(t, n_t, 256, tsin, s));
   FCV_HIP(fcv::gemm_bias_silu_bf16(tsin, 256, B(w.temb_w1), 256, w.temb_b1, n_t, D, 256, t1, D, s));
   FCV_HIP(fcv::gemm_bias_silu_bf16(t1, D, B(w.temb_w2), D, w.temb_b2, n_t, D, D, t2, D, s));
+  FCV_HIP(m->probe_begin(FCV_STAGE_ADALN, -1, s));
   FCV_HIP(fcv::gemm_bias_f32(t2, D, B(w.ada_w), D, w.ada_b, n_t, (int)m->mod_width, D, mod,
                              (int)m->mod_width, (int)m->mod_width, s));
+  FCV_HIP(m->probe_end(FCV_STAGE_ADALN, -1, s));
 
   // input projection + causal conv position embedding (InputEmbedding dit.py:84-98)
   FCV_HIP(fcv::pack_inputs(x, cond, mu, spks, docid, ext_row, R, mel, ain, s));
+  FCV_HIP(m->probe_begin(FCV_STAGE_IN_PROJ, -1, s));
   FCV_HIP(fcv::gemm_bias_f32_bf16(ain, 4 * mel, B(w.in_w), 4 * mel, w.in_b, R, D, 4 * mel, h,
                                   nbuf, D, s));
+  FCV_HIP(m->probe_end(FCV_STAGE_IN_PROJ, -1, s));
+  FCV_HIP(m->probe_begin(FCV_STAGE_CONV, -1, s));
   FCV_HIP(fcv::conv_causal_mish(nbuf, D, B(w.conv1_w), w.conv1_b, d.conv_kernel, pos, R, obuf,
                                 nullptr, s));
+  FCV_HIP(m->probe_end(FCV_STAGE_CONV, -1, s));
   FCV_HIP(fcv::conv_causal_mish(obuf, D, B(w.conv2_w), w.conv2_b, d.conv_kernel, pos, R,
                                 nullptr, h, s));
 
   // transformer blocks (DiTBlock.forward modules.py:516-530)
   for (int l = 0; l < d.depth; ++l) {
     const long base = (long)l * 6 * D;
+    FCV_HIP(m->probe_begin(FCV_STAGE_LN_MOD, l, s));
     FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 0), (int)(base + D),
                                      docid, nbuf, s));
+    FCV_HIP(m->probe_end(FCV_STAGE_LN_MOD, l, s));
+    FCV_HIP(m->probe_begin(FCV_STAGE_QKV, l, s));
     FCV_HIP(fcv::gemm_qkv_rope(nbuf, D, B(w.qkv_w) + (long)l * 3 * D * D, D,
                                w.qkv_b + (long)l * 3 * D, R, D, d.heads, pos, w.rope_cos,
                                w.rope_sin, d.rope_dim, d.max_pos, q, k, vt, m->rp, s));
+    FCV_HIP(m->probe_end(FCV_STAGE_QKV, l, s));
+    FCV_HIP(m->probe_begin(FCV_STAGE_ATTENTION, l, s));
     FCV_HIP(fcv::attention_varlen(q, k, vt, obuf, cu_int, lens, tiles, m->n_tiles, R, m->rp,
                                   d.heads, m->mask_mode == FCV_MASK_CHUNK_CAUSAL ? m->chunk : 0,
                                   s));
+    FCV_HIP(m->probe_end(FCV_STAGE_ATTENTION, l, s));
+    FCV_HIP(m->probe_begin(FCV_STAGE_OUT_PROJ, l, s));
     FCV_HIP(fcv::gemm_gated_residual(obuf, D, B(w.out_w) + (long)l * D * D, D,
                                      w.out_b + (long)l * D, R, D, D, h, D, mod + base + 2 * D,
                                      mod_stride, docid, s));
+    FCV_HIP(m->probe_end(FCV_STAGE_OUT_PROJ, l, s));
     FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 3 * D),
                                      (int)(base + 4 * D), docid, nbuf, s));
+    FCV_HIP(m->probe_begin(FCV_STAGE_FF1, l, s));
     FCV_HIP(fcv::gemm_bias_gelu_bf16(nbuf, D, B(w.ff1_w) + (long)l * F * D, D,
                                      w.ff1_b + (long)l * F, R, F, D, u, F, s));
+    FCV_HIP(m->probe_end(FCV_STAGE_FF1, l, s));
+    FCV_HIP(m->probe_begin(FCV_STAGE_FF2, l, s));
     FCV_HIP(fcv::gemm_gated_residual(u, F, B(w.ff2_w) + (long)l * D * F, F,
                                      w.ff2_b + (long)l * D, R, D, F, h, D, mod + base + 5 * D,
                                      mod_stride, docid, s));
+    FCV_HIP(m->probe_end(FCV_STAGE_FF2, l, s));
   }
 
   // final AdaLN (scale, shift) + proj_out (dit.py:174-175, modules.py:260-265)
   const long fin = (long)d.depth * 6 * D;
   FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(fin + D), (int)fin, docid,
                                    nbuf, s));
+  FCV_HIP(m->probe_begin(FCV_STAGE_PROJ_OUT, -1, s));
   FCV_HIP(fcv::gemm_bias_f32_rowmap(nbuf, D, B(w.proj_w), D, w.proj_b, R, 128, D, v_out, mel,
                                     mel, ext_row, s));
+  FCV_HIP(m->probe_end(FCV_STAGE_PROJ_OUT, -1, s));
   return FCV_OK;
 }
 
@@ -236,6 +292,7 @@ int fcv_dit_create(const FcvDitDims* dims, const FcvDitWeights* weights, FcvDit*
 int fcv_dit_destroy(FcvDit* dit) {
   if (!dit) return FCV_OK;
   dit->drop_graph();
+  dit->drop_probe();
   delete dit;
   return FCV_OK;
 }
@@ -352,6 +409,7 @@ int fcv_dit_forward(FcvDit* m, const float* x, const float* mu, const float* con
   FCV_CHECK(x && mu && cond && spks && t && v_out, FCV_ERR_INVALID,
             "spks and cond are required (null input pointer)");
   FCV_CHECK(n_t == 1 || n_t == m->n_docs, FCV_ERR_INVALID, "n_t must be 1 or n_docs");
+  m->probe_count = 0;
   return run_forward(m, x, mu, cond, spks, t, n_t, v_out, s);
 }
 
@@ -390,10 +448,13 @@ int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const
   FCV_HIP(hipMemcpyAsync(tbuf, t_host, n_steps * sizeof(float), hipMemcpyHostToDevice, s));
 
   auto body = [&]() -> int {
+    m->probe_count = 0;
     for (int step = 0; step < n_steps; ++step) {
       int r = run_forward(m, x, mu, cond, spks, tbuf + step, 1, vbuf, s);
       if (r != FCV_OK) return r;
+      FCV_HIP(m->probe_begin(FCV_STAGE_EULER, -1, s));
       FCV_HIP(fcv::euler_cfg_update(x, vbuf, rcond, mel, dt_host[step], cfg, s));
+      FCV_HIP(m->probe_end(FCV_STAGE_EULER, -1, s));
     }
     return FCV_OK;
   };
@@ -456,6 +517,37 @@ int fcv_unpack_padded(FcvDit* m, const float* src, int32_t batch, int32_t channe
               "document longer than padded_len");
   FCV_HIP(fcv::unpack_padded(src, batch, channels, padded_len, m->at<int32_t>(m->L.cu_ext), dst,
                              s));
+  return FCV_OK;
+}
+
+int fcv_dit_probe_arm(FcvDit* m, int32_t stage, int32_t n_pairs) {
+  FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
+  FCV_CHECK(stage >= 0 && stage < FCV_STAGE_COUNT, FCV_ERR_INVALID, "unknown stage");
+  FCV_CHECK(n_pairs >= 0 && n_pairs <= 4096, FCV_ERR_INVALID, "n_pairs must be in [0, 4096]");
+  m->drop_graph();
+  m->drop_probe();
+  if (n_pairs == 0) return FCV_OK;
+  m->probe_events.resize(2 * n_pairs, nullptr);
+  for (auto& e : m->probe_events) {
+    hipError_t err = hipEventCreate(&e);
+    if (err != hipSuccess) {
+      m->drop_probe();
+      return fail(FCV_ERR_RUNTIME, std::string("hipEventCreate: ") + hipGetErrorString(err));
+    }
+  }
+  m->probe_stage = stage;
+  m->probe_pairs = n_pairs;
+  return FCV_OK;
+}
+
+int fcv_dit_probe_read(FcvDit* m, float* ms_out, int32_t cap, int32_t* n_out) {
+  FCV_CHECK(m && ms_out && n_out, FCV_ERR_INVALID, "null argument");
+  FCV_CHECK(m->probe_stage >= 0, FCV_ERR_STATE, "no probe armed");
+  const int n = std::min(m->probe_count, (int)cap);
+  if (n > 0) FCV_HIP(hipEventSynchronize(m->probe_events[2 * (m->probe_count - 1) + 1]));
+  for (int i = 0; i < n; ++i)
+    FCV_HIP(hipEventElapsedTime(&ms_out[i], m->probe_events[2 * i], m->probe_events[2 * i + 1]));
+  *n_out = m->probe_count;
   return FCV_OK;
 }
 
