@@ -160,29 +160,46 @@ def main() -> int:
     handle = est._require()
 
     K = args.steps
-    _lib.check(lib.fcv_dit_probe_arm(handle, 0, K))  # QKV GEMM of block 0, every step
 
-    def solve():
+    def solve(graph: bool):
         return fcv.solve_euler_packed(est, batch.noise, batch.mu, batch.cond, batch.spks,
                                       batch.lengths, n_steps=K, streaming=batch.streaming,
-                                      use_graph=not args.eager)
+                                      use_graph=graph)
 
-    log("[bench] warm-up (captures the hipGraph)")
+    def probed_eager(stage: int) -> tuple[list[float], float]:
+        """One eager K-step solve with HIP events around `stage` (block 0) every step."""
+        _lib.check(lib.fcv_dit_probe_arm(handle, stage, K))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        solve(False)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        buf = (_lib.c_float * K)()
+        n = _lib.c_int32()
+        _lib.check(lib.fcv_dit_probe_read(handle, buf, K, n))
+        _lib.check(lib.fcv_dit_probe_arm(handle, stage, 0))
+        return [buf[i] for i in range(min(n.value, K))], wall
+
+    log("[bench] warm-up")
     for _ in range(max(1, -(-args.warmup // K))):
-        solve()
+        solve(False)
     torch.cuda.synchronize()
 
-    log(f"[bench] timing {K} steps")
+    # timed region 1: the dominant kernel (QKV GEMM), HIP events on its stream, eager launches
+    log(f"[bench] timing {K} steps eagerly with events around the QKV GEMM")
+    qkv_ms, eager_wall = probed_eager(0)
+    qkv_avg = sum(qkv_ms) / len(qkv_ms)
+
+    # timed region 2: the metric, K steps replayed from one hipGraph (captured before timing)
+    if not args.eager:
+        solve(True)
+        torch.cuda.synchronize()
+    log(f"[bench] timing {K} steps" + ("" if args.eager else " (hipGraph replay)"))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    solve()
+    solve(not args.eager)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    ms = (_lib.c_float * K)()
-    n = _lib.c_int32()
-    _lib.check(lib.fcv_dit_probe_read(handle, ms, K, n))
-    qkv_ms = sorted(ms[i] for i in range(min(n.value, K)))
-    qkv_avg = sum(qkv_ms) / len(qkv_ms)
 
     rows = batch.rows
     flops = fcv.synthetic.flops_per_forward(batch.doc_lengths, batch.streaming)
@@ -194,17 +211,11 @@ def main() -> int:
 
     breakdown = {}
     if not args.no_breakdown:
-        log("[bench] per-stage breakdown (untimed, probe per stage)")
+        log("[bench] per-stage breakdown (eager, events around each stage in block 0)")
         for stage, name in enumerate(_lib.STAGES):
-            _lib.check(lib.fcv_dit_probe_arm(handle, stage, K))
-            solve()
-            torch.cuda.synchronize()
-            buf = (_lib.c_float * K)()
-            _lib.check(lib.fcv_dit_probe_read(handle, buf, K, n))
-            vals = [buf[i] for i in range(min(n.value, K))]
+            vals, _ = probed_eager(stage)
             if vals:
                 breakdown[name] = round(sum(vals) / len(vals), 4)
-        _lib.check(lib.fcv_dit_probe_arm(handle, 0, 0))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -240,6 +251,7 @@ def main() -> int:
         "tflops_per_step": round(flops["total"] / 1e12, 4),
         "roofline": {
             "kernel": "qkv_gemm (fused bias + RoPE + head-major scatter), block 0, every step",
+            "timing": "HIP events on the launch stream around each launch, eager K-step solve",
             "bound": "mfma",
             "achieved": round(achieved, 1),
             "peak": PEAK_BF16_TFLOPS,
@@ -251,6 +263,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "stage_ms": breakdown,
+        "eager_ms_per_step": round(eager_wall * 1e3 / K, 4),
     }
     print(json.dumps(out), flush=True)
     return 0
