@@ -25,6 +25,10 @@ constexpr int TK = 64;          // keys per LDS tile
 constexpr int HD = 64;          // head dim
 constexpr int LDP = 72;         // padded LDS row (bf16 elements)
 
+// v_exp_f32 without the library's denormal range reduction: results below 2^-126 flush to 0,
+// which only drops probabilities that are negligible next to the row maximum's 1.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __global__ __launch_bounds__(256, 2) void attention_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ VT,
     bf16* __restrict__ O, const int32_t* __restrict__ dstart, const int32_t* __restrict__ dlen,
@@ -108,6 +112,11 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
   float m_run = -INFINITY;
   float l_run = 0.0f;
 
+  // keys below wave_lim are visible to every query of this wave: those tiles skip the mask
+  int wave_lim = key_lim;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) wave_lim = min(wave_lim, __shfl_xor(wave_lim, off, kWave));
+
   const int n_kt = (kv_end - kv_begin + TK - 1) / TK;
   fetch(kv_begin);
   stash(0);
@@ -118,7 +127,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
     const int kb = kv_begin + it * TK;
     if (it + 1 < n_kt) fetch(kb + TK);
 
-    // S^T[key][query] for two 32-key halves
+    // S^T[key][query] for two 32-key halves (raw q.k)
     f32x16 s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
@@ -131,39 +140,48 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
       }
     }
 
-    // mask + online softmax (base-2 exponent with the 1/sqrt(64) scale folded in)
+    // online softmax in base 2: p = exp2(s * scale_log2 - m), m the running max of s * scale_log2
     float tmax = -INFINITY;
+    if (kb + TK <= wave_lim) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = kb + kt * 32 + (e >> 2) * 8 + hl * 4 + (e & 3);
-        const bool ok = key < key_lim;
-        float v = ok ? s[kt][e] * scale_log2 : -INFINITY;
-        s[kt][e] = v;
-        tmax = fmaxf(tmax, v);
+        for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[kt][e]);
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = kb + kt * 32 + (e >> 2) * 8 + hl * 4 + (e & 3);
+          s[kt][e] = key < key_lim ? s[kt][e] : -INFINITY;
+          tmax = fmaxf(tmax, s[kt][e]);
+        }
       }
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-    const float m_new = fmaxf(m_run, tmax);
-    const float corr = exp2f(m_run - m_new);
-    m_run = m_new;
+    const float m_new = fmaxf(m_run, tmax * scale_log2);
+    if (__ballot(m_new > m_run)) {
+      // some query of the wave has a new maximum: rescale its partial sums
+      const float corr = fast_exp2(m_run - m_new);
+      l_run *= corr;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc_o[i][e] *= corr;
+      m_run = m_new;
+    }
     float psum = 0.0f;
     bf16x8 pf[4];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        float p = exp2f(s[kt][e] - m_new);
+        const float p = fast_exp2(fmaf(s[kt][e], scale_log2, -m_new));
         psum += p;
         pf[kt * 2 + (e >> 3)][e & 7] = f2bf(p);
       }
     }
-    l_run = l_run * corr + psum;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc_o[i][e] *= corr;
+    l_run += psum;
 
     // O^T[d][q] += V^T[d][key] P^T[key][q]; slot j of step s <-> key
     //   32*(s/2) + 16*(s%2) + 8*(j/4) + 4*hl + j%4  (same rule as the S^T accumulator)
