@@ -4,15 +4,16 @@
 // accumulation on v_mfma_f32_32x32x16_bf16 (on this part the 32x32x16 form sustains ~93% of
 // the bf16 peak in a register loop, the 16x16x32 form ~54%).
 //
-// Main loop.  A workgroup of 2x2 waves owns a 128x128 tile; each wave a 64x64 sub-tile of
-// 2x2 MFMA tiles.  Operands go straight from global memory into LDS with
-// global_load_lds_dwordx4 (no register staging, no ds_write) through a ring of STAGES slices of
-// K = 32: while slice k feeds the MFMAs, slices k+1..k+STAGES-1 are in flight.  One wave-level
-// load fills 1 KB of LDS = 16 rows x 64 B; the 16-byte chunks of a row sit at position
-// chunk ^ ((row >> 2) & 3), so the 16-row fragment reads hit 16 distinct 16-byte bank groups.
-// Default 3 stages = 48 KB of LDS per workgroup, three workgroups per CU (measured slightly
-// ahead of 4 stages x 2 workgroups: tile epilogues of co-resident workgroups overlap more).
-//
+// Main loop.  A workgroup of WM x WN waves owns a BM x BN tile (256x256, 192x256, 128x256 and
+// 256x128 with 8 waves, 128x128 with 4 waves and two workgroups per CU); each wave a sub-tile
+// of 32x32 MFMA tiles.  Operands go straight from global memory into LDS with
+// global_load_lds_dwordx4 (no register staging, no ds_write) through two stages of K = 64: one
+// wave-level copy fills 1 KB of LDS = 8 rows x 128 B, so every L2 request is a full 128-byte
+// line.  The 16-byte chunks of a row sit at a row-rotated position, so 16 consecutive rows read
+// at one chunk index hit 16 distinct 16-byte bank groups.  Inside a slice the fragments of
+// k-step ks+1 are read while the MFMAs of k-step ks run.  The tile shape is chosen per call to
+// balance the last round of tiles over the 256 CUs.
+
 // Operand roles are swapped: the MFMA computes D = W_tile . A_tile^T, so the accumulator of a
 // 32x32 tile holds, in lane l, output row m = l % 32 and four consecutive output columns per
 // register group.  Every epilogue therefore reads and writes 4 consecutive columns of one row
@@ -23,45 +24,58 @@
 // to give each XCD a contiguous range of tiles; inside that range tiles are visited in groups of
 // GROUP_M M-tiles x all N-tiles (M fastest), keeping the group's A rows and W columns inside
 // one XCD's 4 MB L2.
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace fcv {
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 32;
-#ifndef FCV_GEMM_STAGES
-#define FCV_GEMM_STAGES 3
-#endif
-constexpr int STAGES = FCV_GEMM_STAGES;
-constexpr int WG_PER_CU = STAGES == 4 ? 2 : 3;
-constexpr int kThreads = 256;
-constexpr int TM = 2, TN = 2;          // 32x32 MFMA tiles per wave (wave tile 64x64)
-constexpr int A_INSTR = BM / 16 / 4;   // 1 KB DMA instructions per wave per slice
-constexpr int B_INSTR = BN / 16 / 4;
-constexpr int LOADS = A_INSTR + B_INSTR;
+constexpr int BK = 64;  // slice depth: one 128-byte line per operand row
 constexpr int kXcds = 8;
-constexpr int GROUP_M = 8;
+
+// Tile shape.  WM x WN waves; each wave owns (BM/WM) x (BN/WN) outputs as TM x TN MFMA tiles of
+// 32x32.  Two LDS stages of (BM + BN) x 64 bf16.
+template <int BM_, int BN_, int WM_, int WN_>
+struct TileCfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  static constexpr int A_INSTR = BM / 8 / kWaves;  // 1 KB wave-level copies (8 rows) per slice
+  static constexpr int B_INSTR = BN / 8 / kWaves;
+  static constexpr int kLds = 2 * (BM + BN) * BK * 2;
+  static constexpr int kOcc = (160 * 1024) / kLds >= 2 ? 2 : 1;  // workgroups per CU
+  static constexpr int kGroupM = 1024 / BM > 0 ? 1024 / BM : 1;  // ~1024 A rows per L2 group
+  static_assert(BM % (8 * kWaves) == 0 && BN % (8 * kWaves) == 0, "copy split");
+  static_assert(TM * WM * 32 == BM && TN * WN * 32 == BN, "wave tiling");
+};
 
 __device__ __forceinline__ void tile_coords(int bid, int total, int tiles_m, int tiles_n,
-                                            int& tm, int& tn) {
+                                            int group_m, int& tm, int& tn) {
   const int xcd = bid % kXcds, idx = bid / kXcds;
   const int base = total / kXcds, extra = total % kXcds;
   const int t = xcd * base + min(xcd, extra) + idx;
-  const int per_group = GROUP_M * tiles_n;
+  const int per_group = group_m * tiles_n;
   const int g = t / per_group;
-  const int first_m = g * GROUP_M;
-  const int gm = min(GROUP_M, tiles_m - first_m);
+  const int first_m = g * group_m;
+  const int gm = min(group_m, tiles_m - first_m);
   const int r = t - g * per_group;
   tm = first_m + r % gm;
   tn = r / gm;
 }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+// position of 16-byte chunk `chunk` (0..7) in LDS row `row`: rotated by row/2, so 16
+// consecutive rows read at one chunk index hit 16 distinct 16-byte bank groups
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 // Lane-strided 16-byte global -> LDS copy: lane l writes bytes [16 l, 16 l + 16) of `dst`
 // (dst wave-uniform).  Issued as inline asm so the compiler does not treat every later LDS read
 // as dependent on it (it would wait for vmcnt(0) before each one); the K loop orders these copies
 // with explicit vmcnt waits and barriers instead.
+// (m0 is named as a clobber on purpose: the copy's LDS base lives there.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16(const bf16* src, bf16* dst) {
   const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
@@ -69,52 +83,56 @@ __device__ __forceinline__ void lds_dma16(const bf16* src, bf16* dst) {
                : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(src)
                : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
-// s_waitcnt vmcnt(n) (n < 64: bits [3:0] and [15:14]) leaving expcnt / lgkmcnt unconstrained
-#define FCV_WAIT_VMCNT(n) \
-  __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+// s_waitcnt vmcnt(0), leaving expcnt / lgkmcnt unconstrained
+#define FCV_WAIT_VMCNT0() __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8))
 
-template <class Epi>
-__global__ __launch_bounds__(kThreads, WG_PER_CU) void gemm_kernel(const bf16* __restrict__ A, int lda,
-                                                           const bf16* __restrict__ W, int ldw,
-                                                           int M, int N, int K, Epi epi) {
-  __shared__ __attribute__((aligned(1024))) bf16 sA[STAGES][BM * BK];
-  __shared__ __attribute__((aligned(1024))) bf16 sB[STAGES][BN * BK];
+template <class C, class Epi>
+__global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
+    const bf16* __restrict__ A, int lda, const bf16* __restrict__ W, int ldw, int M, int N, int K,
+    Epi epi) {
+  constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN;
+  // operand ring; after the K loop the same bytes stage the epilogue
+  __shared__ __attribute__((aligned(1024))) bf16 smem[2 * (BM + BN) * BK];
+  bf16 (*sA)[BM * BK] = reinterpret_cast<bf16 (*)[BM * BK]>(smem);
+  bf16 (*sB)[BN * BK] = reinterpret_cast<bf16 (*)[BN * BK]>(smem + 2 * BM * BK);
 
   const int tiles_n = N / BN;
   const int tiles_m = (M + BM - 1) / BM;
   int tmi, tni;
-  tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, tmi, tni);
+  tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, C::kGroupM, tmi, tni);
   const int m0 = tmi * BM;
   const int n0 = tni * BN;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wm0 = (wave >> 1) * 64;
-  const int wn0 = (wave & 1) * 64;
+  const int wm0 = (wave / C::WN) * (BM / C::WM);
+  const int wn0 = (wave % C::WN) * (BN / C::WN);
 
-  // per-lane source of each DMA instruction: row r0 + lane/4, swizzled chunk (A rows clamped)
-  const int lrow = lane >> 2;
-  const bf16* a_src[A_INSTR];
-  const bf16* w_src[B_INSTR];
+  // per-lane source of each copy: row r0 + lane / 8, and the chunk that belongs at LDS position
+  // lane % 8 of that row (A rows clamped to M - 1)
+  const int lrow = lane >> 3;
+  const int lpos = lane & 7;
+  const bf16* a_src[C::A_INSTR];
+  const bf16* w_src[C::B_INSTR];
 #pragma unroll
-  for (int i = 0; i < A_INSTR; ++i) {
-    const int row = (wave * A_INSTR + i) * 16 + lrow;
-    a_src[i] = A + (long)min(m0 + row, M - 1) * lda + swz(row, lane & 3) * 8;
+  for (int i = 0; i < C::A_INSTR; ++i) {
+    const int row = (wave * C::A_INSTR + i) * 8 + lrow;
+    a_src[i] = A + (long)min(m0 + row, M - 1) * lda + swz(row, lpos) * 8;
   }
 #pragma unroll
-  for (int i = 0; i < B_INSTR; ++i) {
-    const int row = (wave * B_INSTR + i) * 16 + lrow;
-    w_src[i] = W + (long)(n0 + row) * ldw + swz(row, lane & 3) * 8;
+  for (int i = 0; i < C::B_INSTR; ++i) {
+    const int row = (wave * C::B_INSTR + i) * 8 + lrow;
+    w_src[i] = W + (long)(n0 + row) * ldw + swz(row, lpos) * 8;
   }
-  const int KT = K / BK;
   auto issue = [&](int kt, int stage) {
-    const int koff = min(kt, KT - 1) * BK;  // clamped tail copies keep the vmcnt count fixed
+    const int koff = kt * BK;
 #pragma unroll
-    for (int i = 0; i < A_INSTR; ++i)
-      lds_dma16(a_src[i] + koff, &sA[stage][(wave * A_INSTR + i) * 16 * BK]);
+    for (int i = 0; i < C::A_INSTR; ++i)
+      lds_dma16(a_src[i] + koff, &sA[stage][(wave * C::A_INSTR + i) * 8 * BK]);
 #pragma unroll
-    for (int i = 0; i < B_INSTR; ++i)
-      lds_dma16(w_src[i] + koff, &sB[stage][(wave * B_INSTR + i) * 16 * BK]);
+    for (int i = 0; i < C::B_INSTR; ++i)
+      lds_dma16(w_src[i] + koff, &sB[stage][(wave * C::B_INSTR + i) * 8 * BK]);
   };
 
   f32x16 acc[TM][TN];
@@ -125,69 +143,135 @@ __global__ __launch_bounds__(kThreads, WG_PER_CU) void gemm_kernel(const bf16* _
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-#pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s) issue(s, s);
   const int fr = lane & 31, fh = lane >> 5;
-  int stage = 0;
+  // Two-stage ring.  Iteration kt: wait for this wave's copies of slice kt, barrier (all
+  // copies of slice kt landed, every wave done reading slice kt-1), start slice kt+1 into the
+  // stage slice kt-1 used, then run slice kt's MFMAs.  Inside a slice the fragments of k-step
+  // ks+1 are read from LDS while the MFMAs of k-step ks run.
+  const int KT = K / BK;
+  issue(0, 0);
   for (int kt = 0; kt < KT; ++kt) {
-    FCV_WAIT_VMCNT((STAGES - 2) * LOADS);  // this wave's copies of slice kt have landed
-    __syncthreads();  // ... and every other wave's; slice kt-1 is no longer read
-    issue(kt + STAGES - 1, stage == 0 ? STAGES - 1 : stage - 1);
+    const int stage = kt & 1;
+    FCV_WAIT_VMCNT0();
+    __syncthreads();
+    if (kt + 1 < KT) issue(kt + 1, stage ^ 1);
     const bf16* a_st = sA[stage];
     const bf16* b_st = sB[stage];
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
+    bf16x8 fa[2][TM], fb[2][TN];
+    auto load = [&](int buf, int ks) {
       const int chunk = ks * 2 + fh;
-      bf16x8 fa[TM], fb[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int row = wm0 + i * 32 + fr;
-        fa[i] = *reinterpret_cast<const bf16x8*>(a_st + row * BK + swz(row, chunk) * 8);
+        fa[buf][i] = *reinterpret_cast<const bf16x8*>(a_st + row * BK + swz(row, chunk) * 8);
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int row = wn0 + j * 32 + fr;
-        fb[j] = *reinterpret_cast<const bf16x8*>(b_st + row * BK + swz(row, chunk) * 8);
+        fb[buf][j] = *reinterpret_cast<const bf16x8*>(b_st + row * BK + swz(row, chunk) * 8);
       }
+    };
+    load(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      if (ks + 1 < BK / 16) load((ks + 1) & 1, ks + 1);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(fb[j], fa[i], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(fb[ks & 1][j], fa[ks & 1][i], acc[i][j]);
     }
-    stage = stage == STAGES - 1 ? 0 : stage + 1;
   }
-  FCV_WAIT_VMCNT(0);  // the clamped tail copies land before the workgroup retires
 
-  // lane: output row m0 + wm0 + 32 i + lane % 32; register group g: columns
-  // n0 + wn0 + 32 j + 8 g + 4 (lane / 32) + 0..3
+  // Epilogue.  Accumulator lane l holds output row m0 + wm0 + 32 i + l % 32 and, in register
+  // group g, columns n0 + wn0 + 32 j + 8 g + 4 (l / 32) + 0..3: stored directly, every store
+  // instruction would touch 32 rows.  Instead each wave stages one 32-row block at a time
+  // through its own LDS region (row pitch padded by 16 bytes) and reads it back row-major:
+  // lanes 16 r .. 16 r + 15 then cover TN x 32 consecutive columns of one row, so the epilogue's
+  // stores are contiguous runs of 16 x 16 B (fp32) or 16 x 8 B (bf16).  Epilogues that write a
+  // transposed layout (V^T) keep the direct lane layout, where 32 lanes cover 32 rows.
+  // Each epilogue is split in prepare (every global load of a 32-row block: bias, gates,
+  // residual, row indices, rotary tables) and finish (arithmetic and stores), so the loads of a
+  // block are in flight together instead of waiting behind the previous row's stores.
+  using Ctx = typename Epi::Ctx;
+  constexpr int WCOLS = TN * 32;
+  constexpr int PITCH = WCOLS + 4;  // floats
+  static_assert(C::kWaves * 32 * PITCH * 4 <= (int)sizeof(smem), "epilogue staging");
+  const int col_base = n0 + wn0;
+  if (epi.direct(col_base)) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = m0 + wm0 + i * 32 + fr;
+      Ctx cx[TN][4];
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) cx[j][g] = epi.prepare(row, col_base + j * 32 + g * 8 + fh * 4, M);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                           acc[i][j][4 * g + 3]};
+          epi.finish(v, cx[j][g], row, col_base + j * 32 + g * 8 + fh * 4, M);
+        }
+    }
+    return;
+  }
+  __syncthreads();  // every wave is done reading the operand ring
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * PITCH;
+  constexpr int LANES_PER_ROW = WCOLS / 4;
+  constexpr int ROWS_PER_PASS = 64 / LANES_PER_ROW;
+  constexpr int PASSES = 32 / ROWS_PER_PASS;
+  const int rr = lane / LANES_PER_ROW, rc = (lane % LANES_PER_ROW) * 4;
+  const int col = col_base + rc;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    const int row = m0 + wm0 + i * 32 + fr;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                         acc[i][j][4 * g + 3]};
-        epi(v, row, n0 + wn0 + j * 32 + g * 8 + fh * 4, M);
-      }
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<f32x4*>(stage + fr * PITCH + j * 32 + g * 8 + fh * 4) =
+            f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                  acc[i][j][4 * g + 3]};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    f32x4 v[PASSES];
+    Ctx cx[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int r = p * ROWS_PER_PASS + rr;
+      v[p] = *reinterpret_cast<const f32x4*>(stage + r * PITCH + rc);
+      cx[p] = epi.prepare(m0 + wm0 + i * 32 + r, col, M);
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+      epi.finish(v[p], cx[p], m0 + wm0 + i * 32 + p * ROWS_PER_PASS + rr, col, M);
   }
 }
 
-// ---- epilogues: v = C[row][col0 .. col0+3] (col0 % 4 == 0) ----------------------------------
+// ---- epilogues: v = C[row][col .. col+3] (col % 4 == 0) -------------------------------------
+// prepare(row, col, M) performs the global loads, finish(v, ctx, row, col, M) the stores.
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 add4(const f32x4& v, const float4& b) {
+  return float4{v[0] + b.x, v[1] + b.y, v[2] + b.z, v[3] + b.w};
+}
 
 struct EpiBiasF32Bf16 {
   const float* bias;
   float* out_f32;
   bf16* out_bf16;
   int ldo;
-  __device__ void operator()(const f32x4& v, int row, int col, int M) const {
+  struct Ctx { float4 b; };
+  __device__ bool direct(int) const { return false; }
+  __device__ Ctx prepare(int, int col, int) const { return {ld4(bias + col)}; }
+  __device__ void finish(const f32x4& v, const Ctx& c, int row, int col, int M) const {
     if (row >= M) return;
-    const float4 b = ld4(bias + col);
-    const float4 y = {v[0] + b.x, v[1] + b.y, v[2] + b.z, v[3] + b.w};
+    const float4 y = add4(v, c.b);
     *reinterpret_cast<float4*>(out_f32 + (long)row * ldo + col) = y;
     *reinterpret_cast<bf16x4*>(out_bf16 + (long)row * ldo + col) =
         bf16x4{f2bf(y.x), f2bf(y.y), f2bf(y.z), f2bf(y.w)};
@@ -199,11 +283,14 @@ struct EpiBiasF32 {
   float* out;
   int ldo;
   int n_valid;  // multiple of 4
-  __device__ void operator()(const f32x4& v, int row, int col, int M) const {
+  struct Ctx { float4 b; };
+  __device__ bool direct(int) const { return false; }
+  __device__ Ctx prepare(int, int col, int) const {
+    return {col < n_valid ? ld4(bias + col) : float4{0.f, 0.f, 0.f, 0.f}};
+  }
+  __device__ void finish(const f32x4& v, const Ctx& c, int row, int col, int M) const {
     if (row >= M || col >= n_valid) return;
-    const float4 b = ld4(bias + col);
-    *reinterpret_cast<float4*>(out + (long)row * ldo + col) =
-        float4{v[0] + b.x, v[1] + b.y, v[2] + b.z, v[3] + b.w};
+    *reinterpret_cast<float4*>(out + (long)row * ldo + col) = add4(v, c.b);
   }
 };
 
@@ -213,13 +300,17 @@ struct EpiBiasF32RowMap {
   int ldo;
   int n_valid;  // multiple of 4
   const int32_t* row_map;
-  __device__ void operator()(const f32x4& v, int row, int col, int M) const {
-    if (row >= M || col >= n_valid) return;
-    const int dst = row_map[row];
-    if (dst < 0) return;
-    const float4 b = ld4(bias + col);
-    *reinterpret_cast<float4*>(out + (long)dst * ldo + col) =
-        float4{v[0] + b.x, v[1] + b.y, v[2] + b.z, v[3] + b.w};
+  struct Ctx { float4 b; int dst; };
+  __device__ bool direct(int) const { return false; }
+  __device__ Ctx prepare(int row, int col, int M) const {
+    Ctx c;
+    c.b = col < n_valid ? ld4(bias + col) : float4{0.f, 0.f, 0.f, 0.f};
+    c.dst = row < M ? row_map[row] : -1;
+    return c;
+  }
+  __device__ void finish(const f32x4& v, const Ctx& c, int, int col, int) const {
+    if (c.dst < 0 || col >= n_valid) return;
+    *reinterpret_cast<float4*>(out + (long)c.dst * ldo + col) = add4(v, c.b);
   }
 };
 
@@ -227,12 +318,14 @@ struct EpiBiasSiluBf16 {
   const float* bias;
   bf16* out;
   int ldo;
-  __device__ void operator()(const f32x4& v, int row, int col, int M) const {
+  struct Ctx { float4 b; };
+  __device__ bool direct(int) const { return false; }
+  __device__ Ctx prepare(int, int col, int) const { return {ld4(bias + col)}; }
+  __device__ void finish(const f32x4& v, const Ctx& c, int row, int col, int M) const {
     if (row >= M) return;
-    const float4 b = ld4(bias + col);
+    const float4 y = add4(v, c.b);
     *reinterpret_cast<bf16x4*>(out + (long)row * ldo + col) =
-        bf16x4{f2bf(silu(v[0] + b.x)), f2bf(silu(v[1] + b.y)), f2bf(silu(v[2] + b.z)),
-               f2bf(silu(v[3] + b.w))};
+        bf16x4{f2bf(silu(y.x)), f2bf(silu(y.y)), f2bf(silu(y.z)), f2bf(silu(y.w))};
   }
 };
 
@@ -240,12 +333,15 @@ struct EpiBiasGeluBf16 {
   const float* bias;
   bf16* out;
   int ldo;
-  __device__ void operator()(const f32x4& v, int row, int col, int M) const {
+  struct Ctx { float4 b; };
+  __device__ bool direct(int) const { return false; }
+  __device__ Ctx prepare(int, int col, int) const { return {ld4(bias + col)}; }
+  __device__ void finish(const f32x4& v, const Ctx& c, int row, int col, int M) const {
     if (row >= M) return;
-    const float4 b = ld4(bias + col);
+    const float4 y = add4(v, c.b);
     *reinterpret_cast<bf16x4*>(out + (long)row * ldo + col) =
-        bf16x4{f2bf(gelu_tanh(v[0] + b.x)), f2bf(gelu_tanh(v[1] + b.y)),
-               f2bf(gelu_tanh(v[2] + b.z)), f2bf(gelu_tanh(v[3] + b.w))};
+        bf16x4{f2bf(gelu_tanh(y.x)), f2bf(gelu_tanh(y.y)), f2bf(gelu_tanh(y.z)),
+               f2bf(gelu_tanh(y.w))};
   }
 };
 
@@ -256,14 +352,22 @@ struct EpiGatedResidual {
   const float* gate;  // mod + gate offset
   long mod_stride;
   const int32_t* docid;
-  __device__ void operator()(const f32x4& v, int row, int col, int M) const {
+  struct Ctx { float4 b, g, x; };
+  __device__ bool direct(int) const { return false; }
+  __device__ Ctx prepare(int row, int col, int M) const {
+    Ctx c;
+    c.b = ld4(bias + col);
+    if (row < M) {
+      c.g = ld4(gate + (long)docid[row] * mod_stride + col);
+      c.x = ld4(h + (long)row * ldh + col);
+    }
+    return c;
+  }
+  __device__ void finish(const f32x4& v, const Ctx& c, int row, int col, int M) const {
     if (row >= M) return;
-    const float4 b = ld4(bias + col);
-    const float4 g = ld4(gate + (long)docid[row] * mod_stride + col);
-    float4* dst = reinterpret_cast<float4*>(h + (long)row * ldh + col);
-    const float4 x = *dst;
-    *dst = float4{x.x + g.x * (v[0] + b.x), x.y + g.y * (v[1] + b.y), x.z + g.z * (v[2] + b.z),
-                  x.w + g.w * (v[3] + b.w)};
+    const float4 y = add4(v, c.b);
+    *reinterpret_cast<float4*>(h + (long)row * ldh + col) =
+        float4{c.x.x + c.g.x * y.x, c.x.y + c.g.y * y.y, c.x.z + c.g.z * y.z, c.x.w + c.g.w * y.w};
   }
 };
 
@@ -280,46 +384,105 @@ struct EpiQkvRope {
   bf16* k;
   bf16* vt;
   int rp;
-  __device__ void operator()(const f32x4& v, int row, int col, int M) const {
+  struct Ctx { float4 b; float2 cs, sn; };
+  // V^T columns keep the accumulator lane layout (32 lanes = 32 consecutive rows of vt)
+  __device__ bool direct(int col) const { return col >= 2 * dim; }
+  __device__ Ctx prepare(int row, int col, int M) const {
+    Ctx c;
+    c.b = ld4(bias + col);
+    const int cc = col % dim;
+    if (col < 2 * dim && row < M && cc < rope_dim) {
+      // angles of the interleaved pairs (cc, cc+1), (cc+2, cc+3); pad rows run past the
+      // document, so the position is clamped
+      const int p = min(pos[row], max_pos - 1);
+      const long t = (long)p * (rope_dim >> 1) + (cc >> 1);
+      c.cs = *reinterpret_cast<const float2*>(rope_cos + t);
+      c.sn = *reinterpret_cast<const float2*>(rope_sin + t);
+    }
+    return c;
+  }
+  __device__ void finish(const f32x4& v, const Ctx& cx, int row, int col, int M) const {
     const int which = col / dim;  // 0 q, 1 k, 2 v
     const int c = col - which * dim;
     const int head = c >> 6, d = c & 63;
-    const float4 b = ld4(bias + col);
-    float y[4] = {v[0] + b.x, v[1] + b.y, v[2] + b.z, v[3] + b.w};
+    float4 y = add4(v, cx.b);
     if (which == 2) {
-      // V transposed: vt[head][d + e][row]; rows < rp always (rp covers every M tile)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) vt[((long)head * 64 + d + e) * rp + row] = f2bf(y[e]);
+      // V transposed: vt[head][d + e][row]; rows in [M, rp) get finite copies of row M-1
+      if (row >= rp) return;
+      vt[((long)head * 64 + d) * rp + row] = f2bf(y.x);
+      vt[((long)head * 64 + d + 1) * rp + row] = f2bf(y.y);
+      vt[((long)head * 64 + d + 2) * rp + row] = f2bf(y.z);
+      vt[((long)head * 64 + d + 3) * rp + row] = f2bf(y.w);
       return;
     }
     if (row >= M) return;
     if (c < rope_dim) {
-      // interleaved pairs (d, d+1), (d+2, d+3): (a, b) -> (a cos - b sin, b cos + a sin)
-      const int p = min(pos[row], max_pos - 1);  // pad rows run past the document
-      const int half = rope_dim >> 1;
-#pragma unroll
-      for (int e = 0; e < 4; e += 2) {
-        const float cs = rope_cos[p * half + ((c + e) >> 1)];
-        const float sn = rope_sin[p * half + ((c + e) >> 1)];
-        const float a = y[e], bb = y[e + 1];
-        y[e] = a * cs - bb * sn;
-        y[e + 1] = bb * cs + a * sn;
-      }
+      // (a, b) -> (a cos - b sin, b cos + a sin)
+      const float a0 = y.x, b0 = y.y, a1 = y.z, b1 = y.w;
+      y.x = a0 * cx.cs.x - b0 * cx.sn.x;
+      y.y = b0 * cx.cs.x + a0 * cx.sn.x;
+      y.z = a1 * cx.cs.y - b1 * cx.sn.y;
+      y.w = b1 * cx.cs.y + a1 * cx.sn.y;
     }
     bf16* dst = (which == 0 ? q : k) + ((long)head * rows + row) * 64 + d;
-    *reinterpret_cast<bf16x4*>(dst) = bf16x4{f2bf(y[0]), f2bf(y[1]), f2bf(y[2]), f2bf(y[3])};
+    *reinterpret_cast<bf16x4*>(dst) = bf16x4{f2bf(y.x), f2bf(y.y), f2bf(y.z), f2bf(y.w)};
   }
 };
+
+using Tile256x256 = TileCfg<256, 256, 2, 4>;
+using Tile192x256 = TileCfg<192, 256, 2, 4>;
+using Tile128x256 = TileCfg<128, 256, 2, 4>;
+using Tile256x128 = TileCfg<256, 128, 4, 2>;
+using Tile128x128 = TileCfg<128, 128, 2, 2>;
+
+template <class C, class Epi>
+hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
+                       const Epi& epi, hipStream_t stream) {
+  if (N % C::BN != 0) return hipErrorInvalidValue;
+  const int tiles = ((M + C::BM - 1) / C::BM) * (N / C::BN);
+  hipLaunchKernelGGL((gemm_kernel<C, Epi>), dim3(tiles), dim3(C::kThreads), 0, stream, A, lda, W,
+                     ldw, M, N, K, epi);
+  return hipGetLastError();
+}
+
+// Tile choice: estimated time = (tiles per CU, rounded up) x tile area / per-CU rate, with the
+// rates measured for each shape at large M with the production epilogues (128x128 runs two
+// workgroups per CU, which its rate includes).  The choice only changes which rows and columns
+// share a workgroup: every output element still accumulates its K slices in the same order, so
+// results are bitwise identical for every tile shape (batch invariance holds).
+constexpr int kCus = 256;
+constexpr int kTileShape[5][2] = {{256, 256}, {192, 256}, {128, 256}, {256, 128}, {128, 128}};
+constexpr float kTileRate[5] = {1.0f, 0.97f, 0.88f, 0.81f, 0.87f};
+
+int g_force_tile = -1;  // >= 0 forces a shape (tuning)
+
+inline int choose_tile(int M, int N) {
+  if (g_force_tile >= 0 && N % kTileShape[g_force_tile][1] == 0) return g_force_tile;
+  int best = 4;
+  float best_t = 3.0e38f;
+  for (int c = 0; c < 5; ++c) {
+    const int bm = kTileShape[c][0], bn = kTileShape[c][1];
+    if (N % bn != 0) continue;
+    const long tiles = (long)((M + bm - 1) / bm) * (N / bn);
+    const long per_cu = (tiles + kCus - 1) / kCus;
+    const float t = (float)per_cu * bm * bn / kTileRate[c];
+    if (t < best_t) { best_t = t; best = c; }
+  }
+  return best;
+}
 
 template <class Epi>
 hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
                   const Epi& epi, hipStream_t stream) {
   if (M <= 0) return hipSuccess;
-  if (N % BN != 0 || K % BK != 0 || lda % 8 != 0 || ldw % 8 != 0) return hipErrorInvalidValue;
-  const int tiles = ((M + BM - 1) / BM) * (N / BN);
-  hipLaunchKernelGGL((gemm_kernel<Epi>), dim3(tiles), dim3(kThreads), 0, stream, A, lda, W, ldw,
-                     M, N, K, epi);
-  return hipGetLastError();
+  if (N % 128 != 0 || K % BK != 0 || lda % 8 != 0 || ldw % 8 != 0) return hipErrorInvalidValue;
+  switch (choose_tile(M, N)) {
+    case 0: return launch_tile<Tile256x256>(A, lda, W, ldw, M, N, K, epi, stream);
+    case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream);
+    case 2: return launch_tile<Tile128x256>(A, lda, W, ldw, M, N, K, epi, stream);
+    case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream);
+    default: return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream);
+  }
 }
 
 }  // namespace
