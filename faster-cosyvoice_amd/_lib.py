@@ -55,7 +55,7 @@ SIGNATURES = {
                                   c_void_p]),
     "fcv_unpack_padded": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p,
                                     c_void_p]),
-    "fcv_dit_probe_arm": (c_int32, [c_void_p, c_int32, c_int32]),
+    "fcv_dit_probe_arm": (c_int32, [c_void_p, c_int32, c_int32, c_int32]),
     "fcv_dit_probe_read": (c_int32, [c_void_p, POINTER(c_float), c_int32, POINTER(c_int32)]),
 }
 

@@ -109,6 +109,7 @@ struct FcvDit {
   int probe_stage = -1;
   int probe_pairs = 0;
   int probe_count = 0;
+  int probe_repeat = 1;
   std::vector<hipEvent_t> probe_events;
 
   // graph cache
@@ -131,12 +132,17 @@ struct FcvDit {
     probe_stage = -1;
     probe_pairs = 0;
     probe_count = 0;
+    probe_repeat = 1;
   }
 
   // event pair around one launch of `stage` in block `layer` (-1 = outside the blocks)
   hipError_t probe_begin(int stage, int layer, hipStream_t s) {
     if (stage != probe_stage || layer > 0 || probe_count >= probe_pairs) return hipSuccess;
     return hipEventRecord(probe_events[2 * probe_count], s);
+  }
+  // launches of `stage` in block `layer` to issue: `probe_repeat` while that launch is probed
+  int launches(int stage, int layer) const {
+    return (stage == probe_stage && layer <= 0 && probe_count < probe_pairs) ? probe_repeat : 1;
   }
   hipError_t probe_end(int stage, int layer, hipStream_t s) {
     if (stage != probe_stage || layer > 0 || probe_count >= probe_pairs) return hipSuccess;
@@ -191,19 +197,22 @@ int run_forward_body(FcvDit* m, const float* x, const float* mu, const float* co
   FCV_HIP(fcv::gemm_bias_silu_bf16(tsin, 256, B(w.temb_w1), 256, w.temb_b1, n_t, D, 256, t1, D, s));
   FCV_HIP(fcv::gemm_bias_silu_bf16(t1, D, B(w.temb_w2), D, w.temb_b2, n_t, D, D, t2, D, s));
   FCV_HIP(m->probe_begin(FCV_STAGE_ADALN, -1, s));
-  FCV_HIP(fcv::gemm_bias_f32(t2, D, B(w.ada_w), D, w.ada_b, n_t, (int)m->mod_width, D, mod,
-                             (int)m->mod_width, (int)m->mod_width, s));
+  for (int rep = m->launches(FCV_STAGE_ADALN, -1); rep > 0; --rep)
+    FCV_HIP(fcv::gemm_bias_f32(t2, D, B(w.ada_w), D, w.ada_b, n_t, (int)m->mod_width, D, mod,
+                               (int)m->mod_width, (int)m->mod_width, s));
   FCV_HIP(m->probe_end(FCV_STAGE_ADALN, -1, s));
 
   // input projection + causal conv position embedding (InputEmbedding dit.py:84-98)
   FCV_HIP(fcv::pack_inputs(x, cond, mu, spks, docid, ext_row, R, mel, ain, s));
   FCV_HIP(m->probe_begin(FCV_STAGE_IN_PROJ, -1, s));
-  FCV_HIP(fcv::gemm_bias_f32_bf16(ain, 4 * mel, B(w.in_w), 4 * mel, w.in_b, R, D, 4 * mel, h,
-                                  nbuf, D, s));
+  for (int rep = m->launches(FCV_STAGE_IN_PROJ, -1); rep > 0; --rep)
+    FCV_HIP(fcv::gemm_bias_f32_bf16(ain, 4 * mel, B(w.in_w), 4 * mel, w.in_b, R, D, 4 * mel, h,
+                                    nbuf, D, s));
   FCV_HIP(m->probe_end(FCV_STAGE_IN_PROJ, -1, s));
   FCV_HIP(m->probe_begin(FCV_STAGE_CONV, -1, s));
-  FCV_HIP(fcv::conv_causal_mish(nbuf, D, B(w.conv1_w), w.conv1_b, d.conv_kernel, pos, R, obuf,
-                                nullptr, s));
+  for (int rep = m->launches(FCV_STAGE_CONV, -1); rep > 0; --rep)
+    FCV_HIP(fcv::conv_causal_mish(nbuf, D, B(w.conv1_w), w.conv1_b, d.conv_kernel, pos, R, obuf,
+                                  nullptr, s));
   FCV_HIP(m->probe_end(FCV_STAGE_CONV, -1, s));
   FCV_HIP(fcv::conv_causal_mish(obuf, D, B(w.conv2_w), w.conv2_b, d.conv_kernel, pos, R,
                                 nullptr, h, s));
@@ -212,18 +221,21 @@ int run_forward_body(FcvDit* m, const float* x, const float* mu, const float* co
   for (int l = 0; l < d.depth; ++l) {
     const long base = (long)l * 6 * D;
     FCV_HIP(m->probe_begin(FCV_STAGE_LN_MOD, l, s));
-    FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 0), (int)(base + D),
-                                     docid, nbuf, s));
+    for (int rep = m->launches(FCV_STAGE_LN_MOD, l); rep > 0; --rep)
+      FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 0), (int)(base + D),
+                                       docid, nbuf, s));
     FCV_HIP(m->probe_end(FCV_STAGE_LN_MOD, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_QKV, l, s));
-    FCV_HIP(fcv::gemm_qkv_rope(nbuf, D, B(w.qkv_w) + (long)l * 3 * D * D, D,
-                               w.qkv_b + (long)l * 3 * D, R, D, d.heads, pos, w.rope_cos,
-                               w.rope_sin, d.rope_dim, d.max_pos, q, k, vt, m->rp, s));
+    for (int rep = m->launches(FCV_STAGE_QKV, l); rep > 0; --rep)
+      FCV_HIP(fcv::gemm_qkv_rope(nbuf, D, B(w.qkv_w) + (long)l * 3 * D * D, D,
+                                 w.qkv_b + (long)l * 3 * D, R, D, d.heads, pos, w.rope_cos,
+                                 w.rope_sin, d.rope_dim, d.max_pos, q, k, vt, m->rp, s));
     FCV_HIP(m->probe_end(FCV_STAGE_QKV, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_ATTENTION, l, s));
-    FCV_HIP(fcv::attention_varlen(q, k, vt, obuf, cu_int, lens, tiles, m->n_tiles, R, m->rp,
-                                  d.heads, m->mask_mode == FCV_MASK_CHUNK_CAUSAL ? m->chunk : 0,
-                                  s));
+    for (int rep = m->launches(FCV_STAGE_ATTENTION, l); rep > 0; --rep)
+      FCV_HIP(fcv::attention_varlen(q, k, vt, obuf, cu_int, lens, tiles, m->n_tiles, R, m->rp,
+                                    d.heads, m->mask_mode == FCV_MASK_CHUNK_CAUSAL ? m->chunk : 0,
+                                    s));
     FCV_HIP(m->probe_end(FCV_STAGE_ATTENTION, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_OUT_PROJ, l, s));
     FCV_HIP(fcv::gemm_gated_residual(obuf, D, B(w.out_w) + (long)l * D * D, D,
@@ -233,8 +245,9 @@ int run_forward_body(FcvDit* m, const float* x, const float* mu, const float* co
     FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 3 * D),
                                      (int)(base + 4 * D), docid, nbuf, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_FF1, l, s));
-    FCV_HIP(fcv::gemm_bias_gelu_bf16(nbuf, D, B(w.ff1_w) + (long)l * F * D, D,
-                                     w.ff1_b + (long)l * F, R, F, D, u, F, s));
+    for (int rep = m->launches(FCV_STAGE_FF1, l); rep > 0; --rep)
+      FCV_HIP(fcv::gemm_bias_gelu_bf16(nbuf, D, B(w.ff1_w) + (long)l * F * D, D,
+                                       w.ff1_b + (long)l * F, R, F, D, u, F, s));
     FCV_HIP(m->probe_end(FCV_STAGE_FF1, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_FF2, l, s));
     FCV_HIP(fcv::gemm_gated_residual(u, F, B(w.ff2_w) + (long)l * D * F, F,
@@ -248,8 +261,9 @@ int run_forward_body(FcvDit* m, const float* x, const float* mu, const float* co
   FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(fin + D), (int)fin, docid,
                                    nbuf, s));
   FCV_HIP(m->probe_begin(FCV_STAGE_PROJ_OUT, -1, s));
-  FCV_HIP(fcv::gemm_bias_f32_rowmap(nbuf, D, B(w.proj_w), D, w.proj_b, R, 128, D, v_out, mel,
-                                    mel, ext_row, s));
+  for (int rep = m->launches(FCV_STAGE_PROJ_OUT, -1); rep > 0; --rep)
+    FCV_HIP(fcv::gemm_bias_f32_rowmap(nbuf, D, B(w.proj_w), D, w.proj_b, R, 128, D, v_out, mel,
+                                      mel, ext_row, s));
   FCV_HIP(m->probe_end(FCV_STAGE_PROJ_OUT, -1, s));
   return FCV_OK;
 }
@@ -520,16 +534,25 @@ int fcv_unpack_padded(FcvDit* m, const float* src, int32_t batch, int32_t channe
   return FCV_OK;
 }
 
-int fcv_dit_probe_arm(FcvDit* m, int32_t stage, int32_t n_pairs) {
+int fcv_dit_probe_arm(FcvDit* m, int32_t stage, int32_t n_pairs, int32_t repeat) {
   FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
   FCV_CHECK(stage >= 0 && stage < FCV_STAGE_COUNT, FCV_ERR_INVALID, "unknown stage");
   FCV_CHECK(n_pairs >= 0 && n_pairs <= 4096, FCV_ERR_INVALID, "n_pairs must be in [0, 4096]");
+  FCV_CHECK(repeat >= 1 && repeat <= 64, FCV_ERR_INVALID, "repeat must be in [1, 64]");
+  // stages whose launch accumulates into its output (gated residuals, conv2, Euler) or that
+  // span several launches cannot be repeated
+  const bool idempotent = stage != FCV_STAGE_OUT_PROJ && stage != FCV_STAGE_FF2 &&
+                          stage != FCV_STAGE_EULER && stage != FCV_STAGE_FORWARD;
+  FCV_CHECK(repeat == 1 || idempotent, FCV_ERR_INVALID,
+            "repeat > 1 needs a stage whose launch is idempotent");
   m->drop_graph();
   m->drop_probe();
   if (n_pairs == 0) return FCV_OK;
   m->probe_events.resize(2 * n_pairs, nullptr);
   for (auto& e : m->probe_events) {
-    hipError_t err = hipEventCreate(&e);
+    // timing-only events: no system-scope fence (and its cache write-back) at each record,
+    // so a pair measures the kernel between them, as a kernel trace does
+    hipError_t err = hipEventCreateWithFlags(&e, hipEventDisableSystemFence);
     if (err != hipSuccess) {
       m->drop_probe();
       return fail(FCV_ERR_RUNTIME, std::string("hipEventCreate: ") + hipGetErrorString(err));
@@ -537,6 +560,7 @@ int fcv_dit_probe_arm(FcvDit* m, int32_t stage, int32_t n_pairs) {
   }
   m->probe_stage = stage;
   m->probe_pairs = n_pairs;
+  m->probe_repeat = repeat;
   return FCV_OK;
 }
 
@@ -545,8 +569,10 @@ int fcv_dit_probe_read(FcvDit* m, float* ms_out, int32_t cap, int32_t* n_out) {
   FCV_CHECK(m->probe_stage >= 0, FCV_ERR_STATE, "no probe armed");
   const int n = std::min(m->probe_count, (int)cap);
   if (n > 0) FCV_HIP(hipEventSynchronize(m->probe_events[2 * (m->probe_count - 1) + 1]));
-  for (int i = 0; i < n; ++i)
+  for (int i = 0; i < n; ++i) {
     FCV_HIP(hipEventElapsedTime(&ms_out[i], m->probe_events[2 * i], m->probe_events[2 * i + 1]));
+    ms_out[i] /= (float)m->probe_repeat;
+  }
   *n_out = m->probe_count;
   return FCV_OK;
 }

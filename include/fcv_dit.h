@@ -126,19 +126,23 @@ int fcv_dit_plan_info(const FcvDit* dit, int32_t* rows, int32_t* n_docs, int32_t
 
 /* Kernel timing probe.  No counterpart in the reference (whose only profiling hook is the
  * plan_calls counter, flashinfer_attention.py:61-62); it lets a benchmark time one kernel live
- * inside a (graph-captured) solve.  Arms a probe on `stage`: during every later forward/solve
- * call the library records a HIP event pair around that stage's launch in block 0 (or its one
- * launch for stages outside the blocks), for the first n_pairs launches counted from the start of
- * the call.  n_pairs == 0 disarms.  Arming or disarming drops the captured graph.
- * fcv_dit_probe_read waits for the last pair and writes up to `cap` durations in ms;
- * *n_out = number of pairs recorded by the last call. */
+ * inside a solve.  Arms a probe on `stage`: during every later forward/solve call the library
+ * records a HIP event pair (timing-only events, no system-scope fence) around that stage's
+ * launch in block 0 (or its one launch for stages outside the blocks), for the first n_pairs
+ * launches counted from the start of the call.  With repeat > 1 the probed launch is issued
+ * `repeat` times back to back between the two events, so per-launch event overhead is
+ * amortised; only stages whose launch is idempotent accept repeat > 1 (QKV, attention, FF1,
+ * LN-modulate, conv, AdaLN, input and output projections).  n_pairs == 0 disarms.  Arming or
+ * disarming drops the captured graph.  fcv_dit_probe_read waits for the last pair and writes up
+ * to `cap` per-launch durations in ms (pair time / repeat); *n_out = number of pairs recorded by
+ * the last call. */
 enum {
   FCV_STAGE_QKV = 0, FCV_STAGE_ATTENTION = 1, FCV_STAGE_OUT_PROJ = 2, FCV_STAGE_FF1 = 3,
   FCV_STAGE_FF2 = 4, FCV_STAGE_LN_MOD = 5, FCV_STAGE_CONV = 6, FCV_STAGE_ADALN = 7,
   FCV_STAGE_IN_PROJ = 8, FCV_STAGE_PROJ_OUT = 9, FCV_STAGE_EULER = 10, FCV_STAGE_FORWARD = 11,
   FCV_STAGE_COUNT = 12
 };
-int fcv_dit_probe_arm(FcvDit* dit, int32_t stage, int32_t n_pairs);
+int fcv_dit_probe_arm(FcvDit* dit, int32_t stage, int32_t n_pairs, int32_t repeat);
 int fcv_dit_probe_read(FcvDit* dit, float* ms_out, int32_t cap, int32_t* n_out);
 
 #ifdef __cplusplus
