@@ -119,6 +119,22 @@ def test_calls_before_plan_raise_state_error(fcv, handle):
         _lib.check(rc)
 
 
+def test_probe_arm_validates_stage_and_repeat(fcv, handle):
+    from faster_cosyvoice_amd import _lib
+    lib = _lib.load()
+    st = {name: i for i, name in enumerate(_lib.STAGES)}
+    with pytest.raises(ValueError, match="unknown stage"):
+        _lib.check(lib.fcv_dit_probe_arm(handle, len(_lib.STAGES), 4, 1))
+    with pytest.raises(ValueError, match="repeat must be"):
+        _lib.check(lib.fcv_dit_probe_arm(handle, st["qkv"], 4, 0))
+    # launches that accumulate into their output cannot be repeated inside one event pair
+    for name in ("out_proj", "ff2", "euler", "forward"):
+        with pytest.raises(ValueError, match="idempotent"):
+            _lib.check(lib.fcv_dit_probe_arm(handle, st[name], 4, 2))
+    # disarming needs no device
+    _lib.check(lib.fcv_dit_probe_arm(handle, st["qkv"], 0, 8))
+
+
 def test_workspace_bytes_monotone(fcv, handle):
     from faster_cosyvoice_amd import _lib
     lib = _lib.load()
