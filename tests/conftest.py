@@ -34,3 +34,15 @@ def pytest_configure(config):
 @pytest.fixture(scope="session")
 def fcv():
     return load_package()
+
+
+@pytest.fixture(scope="session")
+def full22(fcv):
+    """The 22-block DiT with seed-0 N(0, 0.02) weights on cuda:0 (GPU tests only)."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from tests.gpu_helpers import make_estimator, say
+    say("[full22] drawing 22-layer weights")
+    sd = fcv.synthetic.random_state_dict(fcv.synthetic.DiTDims(), seed=0)
+    return sd, make_estimator(fcv, sd, depth=22)

@@ -38,13 +38,6 @@ def stress2(fcv):
     return sd, make_estimator(fcv, sd, depth=2)
 
 
-@pytest.fixture(scope="module")
-def full22(fcv):
-    say("[full22] drawing 22-layer weights")
-    sd = fcv.synthetic.random_state_dict(fcv.synthetic.DiTDims(), seed=0)
-    return sd, make_estimator(fcv, sd, depth=22)
-
-
 @pytest.mark.parametrize("streaming", [False, True])
 def test_one_block_300_frames(fcv, streaming):
     """Workload 1 shape (one block, 300 frames) with nonzero gates."""
