@@ -44,20 +44,29 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// tanh-approximated GELU (torch nn.GELU(approximate="tanh")).
+// Hardware transcendentals (v_exp_f32 = 2^x, v_rcp_f32 = 1/x; about 1 ulp each).
+__device__ __forceinline__ float hw_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float hw_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// tanh-approximated GELU (torch nn.GELU(approximate="tanh")):
+//   0.5 x (1 + tanh(u)) = x / (1 + e^(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3).
+// For x -> -inf, e^(-2u) overflows to inf and the result is -0; for x -> +inf it is x.
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
   const float k1 = 0.044715f;
-  float u = k0 * (x + k1 * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(u));
+  const float u = k0 * fmaf(k1 * x, x * x, x);
+  return x * hw_rcp(1.0f + hw_exp2(-2.8853900817779268f * u));  // -2 log2(e) u
 }
 
-// Mish: x * tanh(softplus(x)), softplus with torch's threshold of 20.
+// Mish: x * tanh(softplus(x)).  With e = e^x, tanh(log(1 + e)) = n / (n + 2), n = e (e + 2).
+// Above 20 torch's softplus returns x itself, and tanh(x) rounds to 1 in fp32.
 __device__ __forceinline__ float mish(float x) {
-  float sp = x > 20.0f ? x : log1pf(expf(x));
-  return x * tanhf(sp);
+  if (x > 20.0f) return x;
+  const float e = hw_exp2(1.4426950408889634f * x);
+  const float n = e * (e + 2.0f);
+  return x * n * hw_rcp(n + 2.0f);
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu(float x) { return x * hw_rcp(1.0f + hw_exp2(-1.4426950408889634f * x)); }
 
 }  // namespace fcv

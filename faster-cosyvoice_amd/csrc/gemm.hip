@@ -174,11 +174,15 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
     load(0, 0);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
+      // scheduling fences keep k-step ks+1's LDS reads ahead of k-step ks's MFMAs (left alone,
+      // the scheduler sinks each read next to its first use and waits on it)
       if (ks + 1 < BK / 16) load((ks + 1) & 1, ks + 1);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(fb[ks & 1][j], fa[ks & 1][i], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 

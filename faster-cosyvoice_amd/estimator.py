@@ -245,8 +245,9 @@ class DiTEstimator(nn.Module):
 
     def __del__(self):
         handle = getattr(self, "_handle", None)
-        if handle is not None and _lib._LIB is not None:
-            _lib._LIB.fcv_dit_destroy(handle)
+        lib = getattr(_lib, "_LIB", None) if _lib is not None else None
+        if handle is not None and lib is not None:  # module globals may be gone at exit
+            lib.fcv_dit_destroy(handle)
             self._handle = None
 
     # -- planning ---------------------------------------------------------------------------
