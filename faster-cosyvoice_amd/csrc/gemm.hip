@@ -31,23 +31,29 @@
 namespace fcv {
 namespace {
 
-constexpr int BK = 64;  // slice depth: one 128-byte line per operand row
 constexpr int kXcds = 8;
 
 // Tile shape.  WM x WN waves; each wave owns (BM/WM) x (BN/WN) outputs as TM x TN MFMA tiles of
-// 32x32.  Two LDS stages of (BM + BN) x 64 bf16.
-template <int BM_, int BN_, int WM_, int WN_>
+// 32x32.  A ring of STAGES LDS slices of (BM + BN) x BK bf16; one wave-level copy fills 1 KB =
+// ROWS_PER_COPY rows of one slice.
+template <int BM_, int BN_, int WM_, int WN_, int BK_ = 64, int STAGES_ = 2>
 struct TileCfg {
-  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, BK = BK_, STAGES = STAGES_;
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-  static constexpr int A_INSTR = BM / 8 / kWaves;  // 1 KB wave-level copies (8 rows) per slice
-  static constexpr int B_INSTR = BN / 8 / kWaves;
-  static constexpr int kLds = 2 * (BM + BN) * BK * 2;
+  static constexpr int ROW_CHUNKS = BK / 8;            // 16-byte chunks per slice row
+  static constexpr int ROWS_PER_COPY = 64 / ROW_CHUNKS;
+  static constexpr int A_INSTR = BM / ROWS_PER_COPY / kWaves;  // copies per wave per slice
+  static constexpr int B_INSTR = BN / ROWS_PER_COPY / kWaves;
+  static constexpr int LOADS = A_INSTR + B_INSTR;
+  static constexpr int kLds = STAGES * (BM + BN) * BK * 2;
   static constexpr int kOcc = (160 * 1024) / kLds >= 2 ? 2 : 1;  // workgroups per CU
   static constexpr int kGroupM = 1024 / BM > 0 ? 1024 / BM : 1;  // ~1024 A rows per L2 group
-  static_assert(BM % (8 * kWaves) == 0 && BN % (8 * kWaves) == 0, "copy split");
+  static_assert(BK == 32 || BK == 64, "slice depth");
+  static_assert(STAGES >= 2 && (STAGES - 2) * LOADS < 64, "ring depth");
+  static_assert(BM % (ROWS_PER_COPY * kWaves) == 0 && BN % (ROWS_PER_COPY * kWaves) == 0,
+                "copy split");
   static_assert(TM * WM * 32 == BM && TN * WN * 32 == BN, "wave tiling");
 };
 
@@ -65,9 +71,13 @@ __device__ __forceinline__ void tile_coords(int bid, int total, int tiles_m, int
   tn = r / gm;
 }
 
-// position of 16-byte chunk `chunk` (0..7) in LDS row `row`: rotated by row/2, so 16
-// consecutive rows read at one chunk index hit 16 distinct 16-byte bank groups
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+// position of 16-byte chunk `chunk` in LDS row `row`: rows of 8 chunks (BK 64) rotate by row/2,
+// rows of 4 chunks (BK 32) by row/4, so 16 consecutive rows read at one chunk index hit 16
+// distinct 16-byte bank groups
+template <int BK>
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return BK == 64 ? chunk ^ ((row >> 1) & 7) : chunk ^ ((row >> 2) & 3);
+}
 
 // Lane-strided 16-byte global -> LDS copy: lane l writes bytes [16 l, 16 l + 16) of `dst`
 // (dst wave-uniform).  Issued as inline asm so the compiler does not treat every later LDS read
@@ -85,18 +95,34 @@ __device__ __forceinline__ void lds_dma16(const bf16* src, bf16* dst) {
 }
 #pragma clang diagnostic pop
 
-// s_waitcnt vmcnt(0), leaving expcnt / lgkmcnt unconstrained
-#define FCV_WAIT_VMCNT0() __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8))
+// s_waitcnt vmcnt(n) (n < 64: bits [3:0] and [15:14]), leaving expcnt / lgkmcnt unconstrained
+#define FCV_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+#define FCV_WAIT_VMCNT0() FCV_WAIT_VMCNT(0)
+
+// vmcnt(ahead * L) for a wave-uniform ahead in [0, A]
+template <int L, int A>
+__device__ __forceinline__ void wait_loads_ahead(int ahead) {
+  if constexpr (A > 0) {
+    if (ahead >= A) {
+      FCV_WAIT_VMCNT(A * L);
+      return;
+    }
+    wait_loads_ahead<L, A - 1>(ahead);
+  } else {
+    FCV_WAIT_VMCNT0();
+  }
+}
 
 template <class C, class Epi>
 __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
     const bf16* __restrict__ A, int lda, const bf16* __restrict__ W, int ldw, int M, int N, int K,
     Epi epi) {
-  constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN;
+  constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN, BK = C::BK, S = C::STAGES;
   // operand ring; after the K loop the same bytes stage the epilogue
-  __shared__ __attribute__((aligned(1024))) bf16 smem[2 * (BM + BN) * BK];
+  __shared__ __attribute__((aligned(1024))) bf16 smem[S * (BM + BN) * BK];
   bf16 (*sA)[BM * BK] = reinterpret_cast<bf16 (*)[BM * BK]>(smem);
-  bf16 (*sB)[BN * BK] = reinterpret_cast<bf16 (*)[BN * BK]>(smem + 2 * BM * BK);
+  bf16 (*sB)[BN * BK] = reinterpret_cast<bf16 (*)[BN * BK]>(smem + S * BM * BK);
 
   const int tiles_n = N / BN;
   const int tiles_m = (M + BM - 1) / BM;
@@ -109,31 +135,53 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   const int wm0 = (wave / C::WN) * (BM / C::WM);
   const int wn0 = (wave % C::WN) * (BN / C::WN);
 
-  // per-lane source of each copy: row r0 + lane / 8, and the chunk that belongs at LDS position
-  // lane % 8 of that row (A rows clamped to M - 1)
-  const int lrow = lane >> 3;
-  const int lpos = lane & 7;
+  // per-lane source of each copy: row r0 + lane / ROW_CHUNKS, and the chunk that belongs at LDS
+  // position lane % ROW_CHUNKS of that row (A rows clamped to M - 1)
+  const int lrow = lane / C::ROW_CHUNKS;
+  const int lpos = lane % C::ROW_CHUNKS;
   const bf16* a_src[C::A_INSTR];
   const bf16* w_src[C::B_INSTR];
 #pragma unroll
   for (int i = 0; i < C::A_INSTR; ++i) {
-    const int row = (wave * C::A_INSTR + i) * 8 + lrow;
-    a_src[i] = A + (long)min(m0 + row, M - 1) * lda + swz(row, lpos) * 8;
+    const int row = (wave * C::A_INSTR + i) * C::ROWS_PER_COPY + lrow;
+    a_src[i] = A + (long)min(m0 + row, M - 1) * lda + swz<BK>(row, lpos) * 8;
   }
 #pragma unroll
   for (int i = 0; i < C::B_INSTR; ++i) {
-    const int row = (wave * C::B_INSTR + i) * 8 + lrow;
-    w_src[i] = W + (long)(n0 + row) * ldw + swz(row, lpos) * 8;
+    const int row = (wave * C::B_INSTR + i) * C::ROWS_PER_COPY + lrow;
+    w_src[i] = W + (long)(n0 + row) * ldw + swz<BK>(row, lpos) * 8;
   }
   auto issue = [&](int kt, int stage) {
     const int koff = kt * BK;
 #pragma unroll
     for (int i = 0; i < C::A_INSTR; ++i)
-      lds_dma16(a_src[i] + koff, &sA[stage][(wave * C::A_INSTR + i) * 8 * BK]);
+      lds_dma16(a_src[i] + koff, &sA[stage][(wave * C::A_INSTR + i) * C::ROWS_PER_COPY * BK]);
 #pragma unroll
     for (int i = 0; i < C::B_INSTR; ++i)
-      lds_dma16(w_src[i] + koff, &sB[stage][(wave * C::B_INSTR + i) * 8 * BK]);
+      lds_dma16(w_src[i] + koff, &sB[stage][(wave * C::B_INSTR + i) * C::ROWS_PER_COPY * BK]);
   };
+
+  // Column-only epilogue inputs (bias; gates shared by all rows) are loaded here, before the K
+  // loop: issued after the epilogue's first stores they would wait for those stores to drain
+  // (loads and stores share one counter).  Staged layout: lanes 16r .. 16r + 15 cover the
+  // wave's TN x 32 columns, 4 per lane; direct layout: register group g of MFMA tile j holds
+  // columns 32 j + 8 g + 4 (lane / 32) + 0..3.
+  using Col = typename Epi::Col;
+  constexpr int WCOLS = TN * 32;
+  constexpr int LANES_PER_ROW = WCOLS / 4;
+  const int col_base = n0 + wn0;
+  const bool direct = epi.direct(col_base);
+  const int rc = (lane % LANES_PER_ROW) * 4;
+  Col scol{};
+  Col dcol[TN][4];
+  if (direct) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) dcol[j][g] = epi.column(col_base + j * 32 + g * 8 + (lane >> 5) * 4);
+  } else {
+    scol = epi.column(col_base + rc);
+  }
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -144,17 +192,21 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
   const int fr = lane & 31, fh = lane >> 5;
-  // Two-stage ring.  Iteration kt: wait for this wave's copies of slice kt, barrier (all
-  // copies of slice kt landed, every wave done reading slice kt-1), start slice kt+1 into the
-  // stage slice kt-1 used, then run slice kt's MFMAs.  Inside a slice the fragments of k-step
-  // ks+1 are read from LDS while the MFMAs of k-step ks run.
+  // Ring of S stages.  Iteration kt: wait for this wave's copies of slice kt (the copies of
+  // the up to S-2 later slices already issued may still be in flight; loads complete in order),
+  // barrier (all copies of slice kt landed, every wave done reading slice kt-1), start slice
+  // kt+S-1 into the stage slice kt-1 used, then run slice kt's MFMAs.  Inside a slice the
+  // fragments of k-step ks+1 are read from LDS while the MFMAs of k-step ks run.
   const int KT = K / BK;
-  issue(0, 0);
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < KT) issue(st, st);
+  int stage = 0;
   for (int kt = 0; kt < KT; ++kt) {
-    const int stage = kt & 1;
-    FCV_WAIT_VMCNT0();
+    // slices issued after slice kt: min(S - 2, KT - 1 - kt)
+    wait_loads_ahead<C::LOADS, S - 2>(KT - 1 - kt);
     __syncthreads();
-    if (kt + 1 < KT) issue(kt + 1, stage ^ 1);
+    if (kt + S - 1 < KT) issue(kt + S - 1, stage == 0 ? S - 1 : stage - 1);
     const bf16* a_st = sA[stage];
     const bf16* b_st = sB[stage];
     bf16x8 fa[2][TM], fb[2][TN];
@@ -163,12 +215,12 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int row = wm0 + i * 32 + fr;
-        fa[buf][i] = *reinterpret_cast<const bf16x8*>(a_st + row * BK + swz(row, chunk) * 8);
+        fa[buf][i] = *reinterpret_cast<const bf16x8*>(a_st + row * BK + swz<BK>(row, chunk) * 8);
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int row = wn0 + j * 32 + fr;
-        fb[buf][j] = *reinterpret_cast<const bf16x8*>(b_st + row * BK + swz(row, chunk) * 8);
+        fb[buf][j] = *reinterpret_cast<const bf16x8*>(b_st + row * BK + swz<BK>(row, chunk) * 8);
       }
     };
     load(0, 0);
@@ -184,7 +236,13 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
         for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(fb[ks & 1][j], fa[ks & 1][i], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
     }
+    stage = stage == S - 1 ? 0 : stage + 1;
   }
+
+  // Nothing is in flight here; the explicit wait tells the compiler's counter tracking that the
+  // column loads issued before the loop are complete on every path (with a zero-trip loop path
+  // it would otherwise wait again, for every store, inside each row-guarded store block).
+  FCV_WAIT_VMCNT0();
 
   // Epilogue.  Accumulator lane l holds output row m0 + wm0 + 32 i + l % 32 and, in register
   // group g, columns n0 + wn0 + 32 j + 8 g + 4 (l / 32) + 0..3: stored directly, every store
@@ -193,92 +251,106 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   // lanes 16 r .. 16 r + 15 then cover TN x 32 consecutive columns of one row, so the epilogue's
   // stores are contiguous runs of 16 x 16 B (fp32) or 16 x 8 B (bf16).  Epilogues that write a
   // transposed layout (V^T) keep the direct lane layout, where 32 lanes cover 32 rows.
-  // Each epilogue is split in prepare (every global load of a 32-row block: bias, gates,
-  // residual, row indices, rotary tables) and finish (arithmetic and stores), so the loads of a
-  // block are in flight together instead of waiting behind the previous row's stores.
+  // Row-dependent loads of a block (residual, row indices, rotary tables) are issued together
+  // by prepare before the block's stores in finish; finish computes its values unconditionally
+  // and guards only the stores, so a block waits for its loads once, not once per store.
   using Ctx = typename Epi::Ctx;
-  constexpr int WCOLS = TN * 32;
   constexpr int PITCH = WCOLS + 4;  // floats
   static_assert(C::kWaves * 32 * PITCH * 4 <= (int)sizeof(smem), "epilogue staging");
-  const int col_base = n0 + wn0;
-  if (epi.direct(col_base)) {
+  if (direct) {
+    // direct-layout tiles (V^T) read nothing per row
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int row = m0 + wm0 + i * 32 + fr;
-      Ctx cx[TN][4];
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) cx[j][g] = epi.prepare(row, col_base + j * 32 + g * 8 + fh * 4, M);
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                            acc[i][j][4 * g + 3]};
-          epi.finish(v, cx[j][g], row, col_base + j * 32 + g * 8 + fh * 4, M);
+          epi.finish(v, epi.blank(dcol[j][g]), dcol[j][g], row,
+                     col_base + j * 32 + g * 8 + fh * 4, M);
         }
     }
     return;
   }
   __syncthreads();  // every wave is done reading the operand ring
-  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * PITCH;
-  constexpr int LANES_PER_ROW = WCOLS / 4;
+  float* stg = reinterpret_cast<float*>(smem) + wave * 32 * PITCH;
   constexpr int ROWS_PER_PASS = 64 / LANES_PER_ROW;
   constexpr int PASSES = 32 / ROWS_PER_PASS;
-  const int rr = lane / LANES_PER_ROW, rc = (lane % LANES_PER_ROW) * 4;
+  const int rr = lane / LANES_PER_ROW;
   const int col = col_base + rc;
+  // Two instantiations: tiles whose epilogue reads per-row data wait once per 32-row block,
+  // after issuing that block's loads (the wait also covers the previous block's stores: loads
+  // and stores share one counter); tiles without row data never wait.
+  auto staged = [&](auto loads_c) {
+    constexpr bool kLoads = decltype(loads_c)::value;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<f32x4*>(stage + fr * PITCH + j * 32 + g * 8 + fh * 4) =
-            f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                  acc[i][j][4 * g + 3]};
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    f32x4 v[PASSES];
-    Ctx cx[PASSES];
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(stg + fr * PITCH + j * 32 + g * 8 + fh * 4) =
+              f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                    acc[i][j][4 * g + 3]};
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      f32x4 v[PASSES];
+      Ctx cx[PASSES];
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int r = p * ROWS_PER_PASS + rr;
-      v[p] = *reinterpret_cast<const f32x4*>(stage + r * PITCH + rc);
-      cx[p] = epi.prepare(m0 + wm0 + i * 32 + r, col, M);
+      for (int p = 0; p < PASSES; ++p) {
+        const int r = p * ROWS_PER_PASS + rr;
+        v[p] = *reinterpret_cast<const f32x4*>(stg + r * PITCH + rc);
+        cx[p] = kLoads ? epi.prepare(m0 + wm0 + i * 32 + r, col, M, scol) : epi.blank(scol);
+      }
+      if (kLoads) FCV_WAIT_VMCNT0();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p)
+        epi.finish(v[p], cx[p], scol, m0 + wm0 + i * 32 + p * ROWS_PER_PASS + rr, col, M);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p)
-      epi.finish(v[p], cx[p], m0 + wm0 + i * 32 + p * ROWS_PER_PASS + rr, col, M);
-  }
+  };
+  if (epi.row_loads(col_base, WCOLS))
+    staged(std::true_type{});
+  else
+    staged(std::false_type{});
 }
 
 // ---- epilogues: v = C[row][col .. col+3] (col % 4 == 0) -------------------------------------
-// prepare(row, col, M) performs the global loads, finish(v, ctx, row, col, M) the stores.
+// column(col): loads that depend on the column only (issued before the K loop);
+// row_loads(col0, n): whether columns [col0, col0 + n) need per-row data;
+// prepare(row, col, M, col_ctx): the row-dependent loads; blank(col_ctx): the context when there
+// are none; finish(v, ctx, col_ctx, row, col, M): the arithmetic and the stores.
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ float4 add4(const f32x4& v, const float4& b) {
   return float4{v[0] + b.x, v[1] + b.y, v[2] + b.z, v[3] + b.w};
 }
+struct NoCtx {};
+struct BiasCol { float4 b; };
 
 struct EpiBiasF32Bf16 {
   const float* bias;
   float* out_f32;
   bf16* out_bf16;
   int ldo;
-  struct Ctx { float4 b; };
+  using Col = BiasCol;
+  using Ctx = NoCtx;
+  __device__ bool row_loads(int, int) const { return false; }
+  __device__ Ctx blank(const Col&) const { return {}; }
   __device__ bool direct(int) const { return false; }
-  __device__ Ctx prepare(int, int col, int) const { return {ld4(bias + col)}; }
-  __device__ void finish(const f32x4& v, const Ctx& c, int row, int col, int M) const {
-    if (row >= M) return;
+  __device__ Col column(int col) const { return {ld4(bias + col)}; }
+  __device__ Ctx prepare(int, int, int, const Col&) const { return {}; }
+  __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
+    const bf16x4 yb = {f2bf(y.x), f2bf(y.y), f2bf(y.z), f2bf(y.w)};
+    if (row >= M) return;
     *reinterpret_cast<float4*>(out_f32 + (long)row * ldo + col) = y;
-    *reinterpret_cast<bf16x4*>(out_bf16 + (long)row * ldo + col) =
-        bf16x4{f2bf(y.x), f2bf(y.y), f2bf(y.z), f2bf(y.w)};
+    *reinterpret_cast<bf16x4*>(out_bf16 + (long)row * ldo + col) = yb;
   }
 };
 
@@ -287,14 +359,19 @@ struct EpiBiasF32 {
   float* out;
   int ldo;
   int n_valid;  // multiple of 4
-  struct Ctx { float4 b; };
+  using Col = BiasCol;
+  using Ctx = NoCtx;
+  __device__ bool row_loads(int, int) const { return false; }
+  __device__ Ctx blank(const Col&) const { return {}; }
   __device__ bool direct(int) const { return false; }
-  __device__ Ctx prepare(int, int col, int) const {
+  __device__ Col column(int col) const {
     return {col < n_valid ? ld4(bias + col) : float4{0.f, 0.f, 0.f, 0.f}};
   }
-  __device__ void finish(const f32x4& v, const Ctx& c, int row, int col, int M) const {
+  __device__ Ctx prepare(int, int, int, const Col&) const { return {}; }
+  __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
+    const float4 y = add4(v, c.b);
     if (row >= M || col >= n_valid) return;
-    *reinterpret_cast<float4*>(out + (long)row * ldo + col) = add4(v, c.b);
+    *reinterpret_cast<float4*>(out + (long)row * ldo + col) = y;
   }
 };
 
@@ -304,17 +381,21 @@ struct EpiBiasF32RowMap {
   int ldo;
   int n_valid;  // multiple of 4
   const int32_t* row_map;
-  struct Ctx { float4 b; int dst; };
+  using Col = BiasCol;
+  struct Ctx { int dst; };
+  __device__ bool row_loads(int, int) const { return true; }
+  __device__ Ctx blank(const Col&) const { return {-1}; }
   __device__ bool direct(int) const { return false; }
-  __device__ Ctx prepare(int row, int col, int M) const {
-    Ctx c;
-    c.b = col < n_valid ? ld4(bias + col) : float4{0.f, 0.f, 0.f, 0.f};
-    c.dst = row < M ? row_map[row] : -1;
-    return c;
+  __device__ Col column(int col) const {
+    return {col < n_valid ? ld4(bias + col) : float4{0.f, 0.f, 0.f, 0.f}};
   }
-  __device__ void finish(const f32x4& v, const Ctx& c, int, int col, int) const {
-    if (c.dst < 0 || col >= n_valid) return;
-    *reinterpret_cast<float4*>(out + (long)c.dst * ldo + col) = add4(v, c.b);
+  __device__ Ctx prepare(int row, int, int M, const Col&) const {
+    return {row < M ? row_map[row] : -1};
+  }
+  __device__ void finish(const f32x4& v, const Ctx& x, const Col& c, int, int col, int) const {
+    const float4 y = add4(v, c.b);
+    if (x.dst < 0 || col >= n_valid) return;
+    *reinterpret_cast<float4*>(out + (long)x.dst * ldo + col) = y;
   }
 };
 
@@ -322,14 +403,18 @@ struct EpiBiasSiluBf16 {
   const float* bias;
   bf16* out;
   int ldo;
-  struct Ctx { float4 b; };
+  using Col = BiasCol;
+  using Ctx = NoCtx;
+  __device__ bool row_loads(int, int) const { return false; }
+  __device__ Ctx blank(const Col&) const { return {}; }
   __device__ bool direct(int) const { return false; }
-  __device__ Ctx prepare(int, int col, int) const { return {ld4(bias + col)}; }
-  __device__ void finish(const f32x4& v, const Ctx& c, int row, int col, int M) const {
-    if (row >= M) return;
+  __device__ Col column(int col) const { return {ld4(bias + col)}; }
+  __device__ Ctx prepare(int, int, int, const Col&) const { return {}; }
+  __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
-    *reinterpret_cast<bf16x4*>(out + (long)row * ldo + col) =
-        bf16x4{f2bf(silu(y.x)), f2bf(silu(y.y)), f2bf(silu(y.z)), f2bf(silu(y.w))};
+    const bf16x4 yb = {f2bf(silu(y.x)), f2bf(silu(y.y)), f2bf(silu(y.z)), f2bf(silu(y.w))};
+    if (row >= M) return;
+    *reinterpret_cast<bf16x4*>(out + (long)row * ldo + col) = yb;
   }
 };
 
@@ -337,15 +422,19 @@ struct EpiBiasGeluBf16 {
   const float* bias;
   bf16* out;
   int ldo;
-  struct Ctx { float4 b; };
+  using Col = BiasCol;
+  using Ctx = NoCtx;
+  __device__ bool row_loads(int, int) const { return false; }
+  __device__ Ctx blank(const Col&) const { return {}; }
   __device__ bool direct(int) const { return false; }
-  __device__ Ctx prepare(int, int col, int) const { return {ld4(bias + col)}; }
-  __device__ void finish(const f32x4& v, const Ctx& c, int row, int col, int M) const {
-    if (row >= M) return;
+  __device__ Col column(int col) const { return {ld4(bias + col)}; }
+  __device__ Ctx prepare(int, int, int, const Col&) const { return {}; }
+  __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
-    *reinterpret_cast<bf16x4*>(out + (long)row * ldo + col) =
-        bf16x4{f2bf(gelu_tanh(y.x)), f2bf(gelu_tanh(y.y)), f2bf(gelu_tanh(y.z)),
-               f2bf(gelu_tanh(y.w))};
+    const bf16x4 yb = {f2bf(gelu_tanh(y.x)), f2bf(gelu_tanh(y.y)), f2bf(gelu_tanh(y.z)),
+                       f2bf(gelu_tanh(y.w))};
+    if (row >= M) return;
+    *reinterpret_cast<bf16x4*>(out + (long)row * ldo + col) = yb;
   }
 };
 
@@ -354,24 +443,35 @@ struct EpiGatedResidual {
   float* h;
   int ldh;
   const float* gate;  // mod + gate offset
-  long mod_stride;
+  long mod_stride;    // 0: one gate row shared by every document
   const int32_t* docid;
-  struct Ctx { float4 b, g, x; };
+  struct Col { float4 b, g; };
+  struct Ctx { float4 g, x; };
+  __device__ bool row_loads(int, int) const { return true; }
+  __device__ Ctx blank(const Col& c) const { return {c.g, float4{0.f, 0.f, 0.f, 0.f}}; }
   __device__ bool direct(int) const { return false; }
-  __device__ Ctx prepare(int row, int col, int M) const {
-    Ctx c;
+  __device__ Col column(int col) const {
+    Col c;
     c.b = ld4(bias + col);
-    if (row < M) {
-      c.g = ld4(gate + (long)docid[row] * mod_stride + col);
-      c.x = ld4(h + (long)row * ldh + col);
-    }
+    c.g = mod_stride == 0 ? ld4(gate + col) : float4{0.f, 0.f, 0.f, 0.f};
     return c;
   }
-  __device__ void finish(const f32x4& v, const Ctx& c, int row, int col, int M) const {
-    if (row >= M) return;
+  __device__ Ctx prepare(int row, int col, int M, const Col& c) const {
+    Ctx x;
+    x.g = c.g;
+    x.x = float4{0.f, 0.f, 0.f, 0.f};
+    if (row < M) {
+      if (mod_stride != 0) x.g = ld4(gate + (long)docid[row] * mod_stride + col);
+      x.x = ld4(h + (long)row * ldh + col);
+    }
+    return x;
+  }
+  __device__ void finish(const f32x4& v, const Ctx& x, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
-    *reinterpret_cast<float4*>(h + (long)row * ldh + col) =
-        float4{c.x.x + c.g.x * y.x, c.x.y + c.g.y * y.y, c.x.z + c.g.z * y.z, c.x.w + c.g.w * y.w};
+    const float4 r = {x.x.x + x.g.x * y.x, x.x.y + x.g.y * y.y, x.x.z + x.g.z * y.z,
+                      x.x.w + x.g.w * y.w};
+    if (row >= M) return;
+    *reinterpret_cast<float4*>(h + (long)row * ldh + col) = r;
   }
 };
 
@@ -388,12 +488,18 @@ struct EpiQkvRope {
   bf16* k;
   bf16* vt;
   int rp;
-  struct Ctx { float4 b; float2 cs, sn; };
+  using Col = BiasCol;
+  struct Ctx { float2 cs, sn; };
   // V^T columns keep the accumulator lane layout (32 lanes = 32 consecutive rows of vt)
+  // only the rotated columns (q and k columns < rope_dim) read per-row angles
+  __device__ bool row_loads(int col0, int n) const {
+    return col0 < 2 * dim && col0 % dim < rope_dim && n > 0;
+  }
+  __device__ Ctx blank(const Col&) const { return {{1.0f, 1.0f}, {0.0f, 0.0f}}; }
   __device__ bool direct(int col) const { return col >= 2 * dim; }
-  __device__ Ctx prepare(int row, int col, int M) const {
-    Ctx c;
-    c.b = ld4(bias + col);
+  __device__ Col column(int col) const { return {ld4(bias + col)}; }
+  __device__ Ctx prepare(int row, int col, int M, const Col&) const {
+    Ctx c = {{1.0f, 1.0f}, {0.0f, 0.0f}};  // identity rotation where no angle is loaded
     const int cc = col % dim;
     if (col < 2 * dim && row < M && cc < rope_dim) {
       // angles of the interleaved pairs (cc, cc+1), (cc+2, cc+3); pad rows run past the
@@ -405,31 +511,32 @@ struct EpiQkvRope {
     }
     return c;
   }
-  __device__ void finish(const f32x4& v, const Ctx& cx, int row, int col, int M) const {
+  __device__ void finish(const f32x4& v, const Ctx& cx, const Col& cb, int row, int col,
+                         int M) const {
     const int which = col / dim;  // 0 q, 1 k, 2 v
     const int c = col - which * dim;
     const int head = c >> 6, d = c & 63;
-    float4 y = add4(v, cx.b);
+    float4 y = add4(v, cb.b);
     if (which == 2) {
       // V transposed: vt[head][d + e][row]; rows in [M, rp) get finite copies of row M-1
+      const bf16 v0 = f2bf(y.x), v1 = f2bf(y.y), v2 = f2bf(y.z), v3 = f2bf(y.w);
       if (row >= rp) return;
-      vt[((long)head * 64 + d) * rp + row] = f2bf(y.x);
-      vt[((long)head * 64 + d + 1) * rp + row] = f2bf(y.y);
-      vt[((long)head * 64 + d + 2) * rp + row] = f2bf(y.z);
-      vt[((long)head * 64 + d + 3) * rp + row] = f2bf(y.w);
+      vt[((long)head * 64 + d) * rp + row] = v0;
+      vt[((long)head * 64 + d + 1) * rp + row] = v1;
+      vt[((long)head * 64 + d + 2) * rp + row] = v2;
+      vt[((long)head * 64 + d + 3) * rp + row] = v3;
       return;
     }
+    // (a, b) -> (a cos - b sin, b cos + a sin) on the rotated columns; the angles are only
+    // loaded there, so the other columns select the unrotated values
+    const float a0 = y.x, b0 = y.y, a1 = y.z, b1 = y.w;
+    const float4 yr = {a0 * cx.cs.x - b0 * cx.sn.x, b0 * cx.cs.x + a0 * cx.sn.x,
+                       a1 * cx.cs.y - b1 * cx.sn.y, b1 * cx.cs.y + a1 * cx.sn.y};
+    if (c < rope_dim) y = yr;
+    const bf16x4 yb = {f2bf(y.x), f2bf(y.y), f2bf(y.z), f2bf(y.w)};
     if (row >= M) return;
-    if (c < rope_dim) {
-      // (a, b) -> (a cos - b sin, b cos + a sin)
-      const float a0 = y.x, b0 = y.y, a1 = y.z, b1 = y.w;
-      y.x = a0 * cx.cs.x - b0 * cx.sn.x;
-      y.y = b0 * cx.cs.x + a0 * cx.sn.x;
-      y.z = a1 * cx.cs.y - b1 * cx.sn.y;
-      y.w = b1 * cx.cs.y + a1 * cx.sn.y;
-    }
     bf16* dst = (which == 0 ? q : k) + ((long)head * rows + row) * 64 + d;
-    *reinterpret_cast<bf16x4*>(dst) = bf16x4{f2bf(y.x), f2bf(y.y), f2bf(y.z), f2bf(y.w)};
+    *reinterpret_cast<bf16x4*>(dst) = yb;
   }
 };
 
@@ -442,7 +549,7 @@ using Tile128x128 = TileCfg<128, 128, 2, 2>;
 template <class C, class Epi>
 hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
                        const Epi& epi, hipStream_t stream) {
-  if (N % C::BN != 0) return hipErrorInvalidValue;
+  if (N % C::BN != 0 || K % C::BK != 0) return hipErrorInvalidValue;
   const int tiles = ((M + C::BM - 1) / C::BM) * (N / C::BN);
   hipLaunchKernelGGL((gemm_kernel<C, Epi>), dim3(tiles), dim3(C::kThreads), 0, stream, A, lda, W,
                      ldw, M, N, K, epi);
@@ -479,7 +586,7 @@ template <class Epi>
 hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
                   const Epi& epi, hipStream_t stream) {
   if (M <= 0) return hipSuccess;
-  if (N % 128 != 0 || K % BK != 0 || lda % 8 != 0 || ldw % 8 != 0) return hipErrorInvalidValue;
+  if (N % 128 != 0 || K % 64 != 0 || lda % 8 != 0 || ldw % 8 != 0) return hipErrorInvalidValue;
   switch (choose_tile(M, N)) {
     case 0: return launch_tile<Tile256x256>(A, lda, W, ldw, M, N, K, epi, stream);
     case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream);
