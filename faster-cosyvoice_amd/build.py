@@ -19,7 +19,7 @@ INCLUDE = PKG_DIR.parent / "include"
 LIB_NAME = "libfcvdit.so"
 ARCH = "gfx950"
 
-SOURCES = ["gemm.hip", "attention.hip", "conv.hip", "elementwise.hip", "capi.hip"]
+SOURCES = ["gemm.hip", "gemv.hip", "attention.hip", "conv.hip", "elementwise.hip", "capi.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -608,6 +608,9 @@ hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const f
                          int M, int N, int K, float* out, int ldo, int n_valid,
                          hipStream_t stream) {
   if (n_valid % 4 != 0) return hipErrorInvalidValue;
+  // a few rows (the AdaLN projection of a shared t): reading W is all the work
+  if (n_valid == N && gemv_supported(M, K, lda, ldw))
+    return gemv_bias_f32(A, lda, W, ldw, bias, M, N, K, out, ldo, stream);
   return launch(A, lda, W, ldw, M, N, K, EpiBiasF32{bias, out, ldo, n_valid}, stream);
 }
 
@@ -621,6 +624,8 @@ hipError_t gemm_bias_f32_rowmap(const bf16* A, int lda, const bf16* W, int ldw,
 
 hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, bf16* out, int ldo, hipStream_t stream) {
+  if (gemv_supported(M, K, lda, ldw))
+    return gemv_bias_silu_bf16(A, lda, W, ldw, bias, M, N, K, out, ldo, stream);
   return launch(A, lda, W, ldw, M, N, K, EpiBiasSiluBf16{bias, out, ldo}, stream);
 }
 

@@ -1,0 +1,119 @@
+// Skinny products out[m, n] = f(sum_k W[n, k] a[m, k] + bias[n]) for M <= 4 rows of a: the
+// timestep MLP and the AdaLN projection, whose time is reading W (the concatenated AdaLN
+// weights are 137216 x 1024 bf16 = 281 MB per evaluation).  Bandwidth-bound, so no MFMA: one
+// wave owns 4 rows of W; lane l reads k in [8l, 8l + 8) of every 512-wide k block, so each load
+// instruction covers 1 KB of one W row contiguously; the wave's 4 x M partial sums are reduced
+// with cross-lane shuffles and written by lane 0.
+#include "kernels.hpp"
+
+namespace fcv {
+namespace {
+
+constexpr int kGemvRows = 4;   // W rows per wave
+constexpr int kGemvMaxM = 4;
+
+struct GemvF32 {
+  const float* bias;
+  float* out;
+  int ldo;
+  __device__ void operator()(int m, int n, float s) const { out[(long)m * ldo + n] = s + bias[n]; }
+};
+
+struct GemvSiluBf16 {
+  const float* bias;
+  bf16* out;
+  int ldo;
+  __device__ void operator()(int m, int n, float s) const {
+    out[(long)m * ldo + n] = f2bf(silu(s + bias[n]));
+  }
+};
+
+// K % 512 == 0: lane l holds k = 512 b + 8 l + 0..7 for each of the K / 512 blocks b
+template <int K, int MM, class Epi>
+__global__ __launch_bounds__(256) void gemv_kernel(const bf16* __restrict__ a, int lda,
+                                                   const bf16* __restrict__ W, int ldw, int M,
+                                                   int N, Epi epi) {
+  constexpr int KB = K / 512;
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kGemvRows;
+  if (n0 >= N) return;
+  float av[MM][KB][8];
+#pragma unroll
+  for (int m = 0; m < MM; ++m)
+#pragma unroll
+    for (int b = 0; b < KB; ++b) {
+      const bf16x8 v = m < M ? *reinterpret_cast<const bf16x8*>(a + (long)m * lda + 512 * b + 8 * lane)
+                             : bf16x8{};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) av[m][b][e] = bf2f(v[e]);
+    }
+  bf16x8 wv[kGemvRows][KB];
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+    for (int b = 0; b < KB; ++b)
+      wv[r][b] = *reinterpret_cast<const bf16x8*>(W + (long)min(n0 + r, N - 1) * ldw + 512 * b +
+                                                  8 * lane);
+  float acc[kGemvRows][MM];
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      float s = 0.0f;
+#pragma unroll
+      for (int b = 0; b < KB; ++b)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s = fmaf(bf2f(wv[r][b][e]), av[m][b][e], s);
+      acc[r][m] = wave_sum(s);
+    }
+  if (lane != 0) return;
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+      if (m < M && n0 + r < N) epi(m, n0 + r, acc[r][m]);
+}
+
+template <int K, class Epi>
+hipError_t launch_gemv_k(const bf16* a, int lda, const bf16* W, int ldw, int M, int N,
+                         const Epi& epi, hipStream_t stream) {
+  const unsigned blocks = (unsigned)((N + 4 * kGemvRows - 1) / (4 * kGemvRows));
+  if (M == 1)
+    hipLaunchKernelGGL((gemv_kernel<K, 1, Epi>), dim3(blocks), dim3(256), 0, stream, a, lda, W,
+                       ldw, M, N, epi);
+  else if (M == 2)
+    hipLaunchKernelGGL((gemv_kernel<K, 2, Epi>), dim3(blocks), dim3(256), 0, stream, a, lda, W,
+                       ldw, M, N, epi);
+  else
+    hipLaunchKernelGGL((gemv_kernel<K, kGemvMaxM, Epi>), dim3(blocks), dim3(256), 0, stream, a,
+                       lda, W, ldw, M, N, epi);
+  return hipGetLastError();
+}
+
+template <class Epi>
+hipError_t launch_gemv(const bf16* a, int lda, const bf16* W, int ldw, int M, int N, int K,
+                       const Epi& epi, hipStream_t stream) {
+  if (K == 1024) return launch_gemv_k<1024>(a, lda, W, ldw, M, N, epi, stream);
+  if (K == 512) return launch_gemv_k<512>(a, lda, W, ldw, M, N, epi, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool gemv_supported(int M, int K, int lda, int ldw) {
+  return M >= 1 && M <= kGemvMaxM && (K == 1024 || K == 512) && lda % 8 == 0 && ldw % 8 == 0;
+}
+
+hipError_t gemv_bias_f32(const bf16* a, int lda, const bf16* W, int ldw, const float* bias, int M,
+                         int N, int K, float* out, int ldo, hipStream_t stream) {
+  if (!gemv_supported(M, K, lda, ldw)) return hipErrorInvalidValue;
+  return launch_gemv(a, lda, W, ldw, M, N, K, GemvF32{bias, out, ldo}, stream);
+}
+
+hipError_t gemv_bias_silu_bf16(const bf16* a, int lda, const bf16* W, int ldw, const float* bias,
+                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream) {
+  if (!gemv_supported(M, K, lda, ldw)) return hipErrorInvalidValue;
+  return launch_gemv(a, lda, W, ldw, M, N, K, GemvSiluBf16{bias, out, ldo}, stream);
+}
+
+}  // namespace fcv

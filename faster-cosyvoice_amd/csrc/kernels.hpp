@@ -48,6 +48,15 @@ hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const f
                          const float* rope_sin, int rope_dim, int max_pos, bf16* q, bf16* k,
                          bf16* vt, int rp, hipStream_t stream);
 
+// ---- skinny products (M <= 4 rows, K in {512, 1024}): bandwidth-bound, no MFMA -----------
+bool gemv_supported(int M, int K, int lda, int ldw);
+// out[m, n] = acc + bias[n]
+hipError_t gemv_bias_f32(const bf16* a, int lda, const bf16* W, int ldw, const float* bias, int M,
+                         int N, int K, float* out, int ldo, hipStream_t stream);
+// out[m, n] = bf16(silu(acc + bias[n]))
+hipError_t gemv_bias_silu_bf16(const bf16* a, int lda, const bf16* W, int ldw, const float* bias,
+                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream);
+
 // ---- attention ----------------------------------------------------------------------------
 // Varlen attention, head_dim 64.  Document d starts at row doc_start[d] (a multiple of 8)
 // and has doc_len[d] real rows; tiles[i] = {doc, first query row}.

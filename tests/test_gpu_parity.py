@@ -89,12 +89,21 @@ def test_ragged_docs_two_blocks(fcv, stress2, streaming):
 
 
 def test_shared_t_equals_per_doc_t(fcv, stress2):
+    """One shared t vs the same t per document.  Up to 4 t rows the time MLP and the AdaLN
+    projection take the same bandwidth-bound path either way (bitwise equal); with more rows
+    they run on the MFMA GEMM, whose fp32 summation order differs, and the bf16 rounding of the
+    time embedding then flips in a few places, so the outputs agree to about 1e-3."""
     sd, est = stress2
     lengths = [50, 70]
     x, mu, cond, spks, _ = random_packed(lengths, seed=3)
     a = est.forward_packed(x, mu, cond, spks, torch.tensor([0.3]), lengths)
     b = est.forward_packed(x, mu, cond, spks, torch.tensor([0.3, 0.3]), lengths)
     assert torch.equal(a, b)
+    lengths = [50, 70, 9, 33, 64, 20]
+    x, mu, cond, spks, _ = random_packed(lengths, seed=3)
+    a = est.forward_packed(x, mu, cond, spks, torch.tensor([0.3]), lengths).cpu()
+    b = est.forward_packed(x, mu, cond, spks, torch.full((6,), 0.3), lengths).cpu()
+    assert rel_l2(a, b) < 5e-3
 
 
 def test_padded_dropin_matches_packed(fcv, stress2):
