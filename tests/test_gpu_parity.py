@@ -8,6 +8,7 @@ weights the GPU uses, the remaining error is activation rounding only and the bo
 from __future__ import annotations
 
 from pathlib import Path
+from types import SimpleNamespace
 
 import numpy as np
 import pytest
@@ -121,6 +122,59 @@ def test_padded_dropin_matches_packed(fcv, stress2):
     assert torch.equal(O.pack(out, lengths), packed)
     for b, n in enumerate(lengths):
         assert torch.all(out[b, :, n:] == 0)
+
+
+def test_solve_euler_batched_dropin(fcv, stress2):
+    """The padded drop-in solver (signature of flashinfer_flow.py:16-74) gives the packed
+    solve's rows on valid frames and leaves padded frames at their noise, as the reference
+    does (its estimator returns zeros there, so dt * dphi is zero)."""
+    sd, est = stress2
+    b = fcv.synthetic.make_batch("dropin", [40, 25, 33], [10, 5, 8], seed=12)
+    pad = b.padded()
+    dev = "cuda:0"
+    decoder = SimpleNamespace(estimator=est, inference_cfg_rate=0.7)
+    out = fcv.solve_euler_batched(decoder, pad["noise"].to(dev), pad["mu"].to(dev),
+                                  pad["mask"].to(dev), pad["spks"].to(dev), pad["cond"].to(dev),
+                                  num_timesteps=4).cpu()
+    ref = fcv.solve_euler_packed(est, b.noise, b.mu, b.cond, b.spks, b.lengths, n_steps=4).cpu()
+    assert torch.equal(O.pack(out, b.lengths), ref)
+    for i, n in enumerate(b.lengths):
+        assert torch.equal(out[i, :, n:], pad["noise"][i, :, n:])
+
+
+def test_apply_mi355x_installs_estimator(fcv, stress2):
+    """apply_mi355x (the apply_flashinfer counterpart, flashinfer_dit.py:951-988) reads the
+    replaced estimator's shape and state dict under the reference's names and installs an
+    estimator that computes exactly what one built directly from that state dict computes."""
+    sd, est = stress2
+
+    class _Attn(torch.nn.Module):
+        heads = 16
+
+    class _Block(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.attn = _Attn()
+
+    class _ReferenceDiT(torch.nn.Module):
+        static_chunk_size = 50
+
+        def __init__(self):
+            super().__init__()
+            self.transformer_blocks = torch.nn.ModuleList([_Block() for _ in range(2)])
+            self.proj_out = torch.nn.Linear(1024, 80, device="meta")
+
+        def state_dict(self, *args, **kwargs):
+            return dict(sd)
+
+    model = SimpleNamespace(flow=SimpleNamespace(decoder=SimpleNamespace(
+        estimator=_ReferenceDiT())))
+    new = fcv.apply_mi355x(model)
+    assert model.flow.decoder.estimator is new
+    lengths = [60, 45]
+    x, mu, cond, spks, t = random_packed(lengths, seed=8)
+    assert torch.equal(new.forward_packed(x, mu, cond, spks, t, lengths),
+                       est.forward_packed(x, mu, cond, spks, t, lengths))
 
 
 def test_missing_inputs_raise(fcv, stress2):
