@@ -5,9 +5,9 @@
 // The 128 + taps - 1 input rows of the group's 64 channels are staged in LDS once; every tap
 // j reads the same window shifted by j rows, so no im2col buffer exists.  Each tap's 64x64
 // weight slice streams through an LDS double buffer.  Packed documents are handled per row:
-// the A fragment of output row r at tap j is zeroed when the input row lies before r's
+// the input fragment of output row r at tap j is zeroed when the input row lies before r's
 // document start, i.e. when pos[r] + j < taps - 1 (the per-document left zero padding of
-// the reference's F.pad).  4 waves x 32 rows x 64 output channels, MFMA 16x16x32 bf16.
+// the reference's F.pad).
 #include "kernels.hpp"
 
 namespace fcv {
@@ -15,18 +15,30 @@ namespace {
 
 constexpr int TM = 128;       // output rows per workgroup
 constexpr int CG = 64;        // channels per group
-constexpr int LDP = CG + 8;   // padded LDS row
+constexpr int LDP = CG + 8;   // padded LDS row (bf16): 16 consecutive rows hit distinct banks
 constexpr int MAX_TAPS = 31;
 constexpr int WIN = TM + MAX_TAPS - 1;
+constexpr int SPITCH = CG + 4;  // fp32 staging row
+constexpr int X_BYTES = WIN * LDP * 2;
+constexpr int W_BYTES = 2 * CG * LDP * 2;
+constexpr int STAGE_BYTES = 4 * 32 * SPITCH * 4;
+constexpr int SMEM_BYTES = X_BYTES + W_BYTES > STAGE_BYTES ? X_BYTES + W_BYTES : STAGE_BYTES;
 
+// 4 waves x 32 output rows x 64 output channels; MFMA 32x32x16 with the weights as the A
+// operand, so lane l accumulates output row l % 32 and, in register group g of channel tile t,
+// channels 32 t + 8 g + 4 (l / 32) + 0..3.  The epilogue stages each wave's 32 x 64 block
+// through LDS and reads it back row-major (16 lanes per row), so stores are contiguous runs of
+// 128 B (bf16 out) or 256 B (fp32 residual); the residual form issues all its h loads before
+// its first store.
 __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x, int C,
                                                       const bf16* __restrict__ w,
                                                       const float* __restrict__ bias, int taps,
                                                       const int32_t* __restrict__ pos, int rows,
                                                       bf16* __restrict__ out_bf16,
                                                       float* __restrict__ h) {
-  __shared__ __attribute__((aligned(16))) bf16 sX[WIN][LDP];
-  __shared__ __attribute__((aligned(16))) bf16 sW[2][CG][LDP];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM_BYTES];
+  bf16 (*sX)[LDP] = reinterpret_cast<bf16 (*)[LDP]>(smem);
+  bf16 (*sW)[CG][LDP] = reinterpret_cast<bf16 (*)[CG][LDP]>(smem + X_BYTES);
 
   const int m0 = blockIdx.x * TM;
   const int g = blockIdx.y;
@@ -57,21 +69,18 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
       *reinterpret_cast<bf16x8*>(&sW[buf][lw_r + 32 * i][chunk_c]) = rw[i];
   };
 
-  // rows owned by this lane in its two 16-row MFMA tiles
-  const int fr = lane & 15;
-  const int fk = (lane >> 4) * 8;
-  int lrow[2], lpos[2];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    lrow[mt] = wave * 32 + mt * 16 + fr;  // row inside the tile
-    lpos[mt] = pos[min(m0 + lrow[mt], rows - 1)];
-  }
+  // output row of this lane (B operand row) and its document position
+  const int fr = lane & 31, fh = lane >> 5;
+  const int lrow = wave * 32 + fr;
+  const int lpos = pos[min(m0 + lrow, rows - 1)];
+  const int col_lane = (lane & 15) * 4;  // epilogue: 4 channels of one row per lane
+  const float4 bias4 = *reinterpret_cast<const float4*>(bias + g * CG + col_lane);
 
-  f32x4 acc[2][4];
+  f32x16 acc[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int e = 0; e < 16; ++e) acc[t][e] = 0.0f;
 
   fetch(0);
   stash(0);
@@ -80,41 +89,54 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
   for (int j = 0; j < taps; ++j) {
     const int cur = j & 1;
     if (j + 1 < taps) fetch(j + 1);
+    // rows before the row's document start read as zero (per-document causal padding)
+    const bool live = lpos + j >= halo;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      bf16x8 fa[2], fb[4];
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(&sX[lrow + j][ks * 16 + fh * 8]);
+      const bf16x8 xb = live ? v : zero8;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        bf16x8 v = *reinterpret_cast<const bf16x8*>(&sX[lrow[mt] + j][ks * 32 + fk]);
-        fa[mt] = (lpos[mt] + j >= halo) ? v : zero8;
+      for (int t = 0; t < 2; ++t) {
+        const bf16x8 wa = *reinterpret_cast<const bf16x8*>(&sW[cur][t * 32 + fr][ks * 16 + fh * 8]);
+        acc[t] = mfma32(wa, xb, acc[t]);
       }
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        fb[nt] = *reinterpret_cast<const bf16x8*>(&sW[cur][nt * 16 + fr][ks * 32 + fk]);
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = mfma16(fa[mt], fb[nt], acc[mt][nt]);
     }
     if (j + 1 < taps) stash(cur ^ 1);
     __syncthreads();
   }
 
+  // epilogue (the loop's last barrier freed the window and weight buffers)
+  float* stage = reinterpret_cast<float*>(smem) + wave * 32 * SPITCH;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int row0 = m0 + wave * 32 + mt * 16 + (lane >> 4) * 4;
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int col = g * CG + nt * 16 + fr;
-      const float b = bias[col];
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<f32x4*>(stage + fr * SPITCH + t * 32 + q * 8 + fh * 4) =
+          f32x4{acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]};
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int col = g * CG + col_lane;
+  f32x4 v[8];
+  float4 hv[8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = row0 + r;
-        if (row >= rows) continue;
-        const float y = mish(acc[mt][nt][r] + b);
-        if (out_bf16) out_bf16[(long)row * C + col] = f2bf(y);
-        if (h) h[(long)row * C + col] += y;
-      }
+  for (int p = 0; p < 8; ++p) {
+    const int r = p * 4 + (lane >> 4);
+    v[p] = *reinterpret_cast<const f32x4*>(stage + r * SPITCH + col_lane);
+    const int row = min(m0 + wave * 32 + r, rows - 1);
+    if (h) hv[p] = *reinterpret_cast<const float4*>(h + (long)row * C + col);
+  }
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int row = m0 + wave * 32 + p * 4 + (lane >> 4);
+    const float4 y = {mish(v[p][0] + bias4.x), mish(v[p][1] + bias4.y), mish(v[p][2] + bias4.z),
+                      mish(v[p][3] + bias4.w)};
+    if (h) {
+      const float4 r4 = {hv[p].x + y.x, hv[p].y + y.y, hv[p].z + y.z, hv[p].w + y.w};
+      if (row < rows) *reinterpret_cast<float4*>(h + (long)row * C + col) = r4;
+    } else {
+      const bf16x4 yb = {f2bf(y.x), f2bf(y.y), f2bf(y.z), f2bf(y.w)};
+      if (row < rows) *reinterpret_cast<bf16x4*>(out_bf16 + (long)row * C + col) = yb;
     }
   }
 }

@@ -5,11 +5,11 @@
 // the bf16 peak in a register loop, the 16x16x32 form ~54%).
 //
 // Main loop.  A workgroup of WM x WN waves owns a BM x BN tile (256x256, 192x256, 128x256 and
-// 256x128 with 8 waves, 128x128 with 4 waves and two workgroups per CU); each wave a sub-tile
-// of 32x32 MFMA tiles.  Operands go straight from global memory into LDS with
-// global_load_lds_dwordx4 (no register staging, no ds_write) through two stages of K = 64: one
-// wave-level copy fills 1 KB of LDS = 8 rows x 128 B, so every L2 request is a full 128-byte
-// line.  The 16-byte chunks of a row sit at a row-rotated position, so 16 consecutive rows read
+// 256x128 with 8 waves, 128x128 and 32x128 with 4 waves, several workgroups per CU); each wave
+// a sub-tile of 32x32 MFMA tiles.  Operands go straight from global memory into LDS with
+// global_load_lds_dwordx4 (no register staging, no ds_write) through a ring of slices (by
+// default two stages of K = 64: one wave-level copy fills 1 KB of LDS = 8 rows x 128 B, so every
+// L2 request is a full 128-byte line).  The 16-byte chunks of a row sit at a row-rotated position, so 16 consecutive rows read
 // at one chunk index hit 16 distinct 16-byte bank groups.  Inside a slice the fragments of
 // k-step ks+1 are read while the MFMAs of k-step ks run.  The tile shape is chosen per call to
 // balance the last round of tiles over the 256 CUs.
@@ -545,6 +545,7 @@ using Tile192x256 = TileCfg<192, 256, 2, 4>;
 using Tile128x256 = TileCfg<128, 256, 2, 4>;
 using Tile256x128 = TileCfg<256, 128, 4, 2>;
 using Tile128x128 = TileCfg<128, 128, 2, 2>;
+using Tile32x128 = TileCfg<32, 128, 1, 4>;
 
 template <class C, class Epi>
 hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
@@ -558,12 +559,14 @@ hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, in
 
 // Tile choice: estimated time = (tiles per CU, rounded up) x tile area / per-CU rate, with the
 // rates measured for each shape at large M with the production epilogues (128x128 runs two
-// workgroups per CU, which its rate includes).  The choice only changes which rows and columns
+// workgroups per CU, which its rate includes; 32x128 is rated low so it only wins when the
+// larger shapes leave most CUs idle, as for the 128-column output projection).  The choice only changes which rows and columns
 // share a workgroup: every output element still accumulates its K slices in the same order, so
 // results are bitwise identical for every tile shape (batch invariance holds).
 constexpr int kCus = 256;
-constexpr int kTileShape[5][2] = {{256, 256}, {192, 256}, {128, 256}, {256, 128}, {128, 128}};
-constexpr float kTileRate[5] = {1.0f, 0.97f, 0.88f, 0.81f, 0.87f};
+constexpr int kTileShape[6][2] = {{256, 256}, {192, 256}, {128, 256}, {256, 128}, {128, 128},
+                                   {32, 128}};
+constexpr float kTileRate[6] = {1.0f, 0.97f, 0.88f, 0.81f, 0.87f, 0.45f};
 
 int g_force_tile = -1;  // >= 0 forces a shape (tuning)
 
@@ -571,7 +574,7 @@ inline int choose_tile(int M, int N) {
   if (g_force_tile >= 0 && N % kTileShape[g_force_tile][1] == 0) return g_force_tile;
   int best = 4;
   float best_t = 3.0e38f;
-  for (int c = 0; c < 5; ++c) {
+  for (int c = 0; c < 6; ++c) {
     const int bm = kTileShape[c][0], bn = kTileShape[c][1];
     if (N % bn != 0) continue;
     const long tiles = (long)((M + bm - 1) / bm) * (N / bn);
@@ -592,6 +595,7 @@ hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, 
     case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream);
     case 2: return launch_tile<Tile128x256>(A, lda, W, ldw, M, N, K, epi, stream);
     case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream);
+    case 5: return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream);
     default: return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream);
   }
 }
