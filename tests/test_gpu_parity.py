@@ -89,6 +89,22 @@ def test_ragged_docs_two_blocks(fcv, stress2, streaming):
         off += n
 
 
+@pytest.mark.parametrize("streaming", [False, True])
+def test_long_document(fcv, stress2, streaming):
+    """One 2500-frame document next to a short one: 40 key tiles per query tile, the long-sequence
+    regime of the 128-document workload, checked against the oracle directly."""
+    sd, est = stress2
+    lengths = [2500, 37]
+    x, mu, cond, spks, t = random_packed(lengths, seed=13)
+    say(f"[long_doc] streaming={streaming} GPU forward")
+    v = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming).cpu()
+    say(f"[long_doc] streaming={streaming} oracle forward")
+    ref = oracle_packed(bf16_weights(sd), x, mu, cond, spks, t, lengths, streaming)
+    e_long, e_short = rel_l2(v[:2500], ref[:2500]), rel_l2(v[2500:], ref[2500:])
+    say(f"[long_doc] streaming={streaming} rel_l2 long {e_long:.2e} short {e_short:.2e}")
+    assert e_long <= BF16_W_TOL and e_short <= BF16_W_TOL
+
+
 def test_shared_t_equals_per_doc_t(fcv, stress2):
     """One shared t vs the same t per document.  Up to 4 t rows the time MLP and the AdaLN
     projection take the same bandwidth-bound path either way (bitwise equal); with more rows
