@@ -30,6 +30,19 @@ def test_library_exports_every_declared_symbol(fcv):
     assert set(declared) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
 
 
+def test_missing_library_fails_loudly(fcv, monkeypatch, tmp_path):
+    """No CPU fallback: without the built HIP library the estimator cannot be used at all."""
+    from faster_cosyvoice_amd import _lib
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libfcvdit.so")
+    with pytest.raises(ImportError, match="only compute path"):
+        _lib.load()
+    # and an estimator never runs on the CPU instead
+    est = fcv.DiTEstimator(depth=1, device="cpu")
+    with pytest.raises(ValueError, match="GPU device"):
+        est.finalize_weights()
+
+
 def test_struct_layouts(fcv):
     from faster_cosyvoice_amd import _lib
     assert ctypes.sizeof(_lib.FcvDitDims) == 10 * 4
