@@ -124,6 +124,65 @@ def measured_traffic(workload: str) -> dict | None:
     return rec if rec.get("workload") == workload else None
 
 
+PEAK_FP32_TFLOPS = 157.3      # MI355X dense fp32 matrix peak
+FRONTEND_REPEAT = 20
+
+
+def frontend_leg(fcv, batch, dev, cpu: bool) -> dict:
+    """The Flow front-end (tokens -> packed mu rows) for the workload's requests: the
+    three-kernel token-features call timed with HIP events on the launch stream over
+    FRONTEND_REPEAT back-to-back calls on device-resident ids, plus the fp32 oracle on the
+    host for the same requests (rank 0, one core budget of a few seconds)."""
+    import torch
+    dims = fcv.synthetic.FlowDims()
+    sd = fcv.synthetic.random_flow_state_dict(dims, seed=0)
+    fe = fcv.FlowFrontEnd(device=dev)
+    fe.load_reference_state_dict(sd)
+    fe.finalize_weights()
+    g = torch.Generator().manual_seed(5)
+    n_tok = [(n + dims.token_mel_ratio - 1) // dims.token_mel_ratio for n in batch.lengths]
+    token_list = [torch.randint(0, dims.vocab, (n,), generator=g).tolist() for n in n_tok]
+    tokens = torch.tensor([v for t in token_list for v in t], dtype=torch.int32, device=dev)
+    out = torch.empty(dims.token_mel_ratio * sum(n_tok), dims.feat, device=dev)
+    for _ in range(3):
+        fe.token_features_device(tokens, n_tok, out=out)
+    stream = torch.cuda.current_stream(dev)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(FRONTEND_REPEAT):
+        fe.token_features_device(tokens, n_tok, out=out)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / FRONTEND_REPEAT
+    tokens_total = sum(n_tok)
+    flop_per_token = 2 * (dims.channels * (dims.lookahead + 1) * dims.feat
+                          + dims.feat * 3 * dims.channels)
+    tflops = flop_per_token * tokens_total / (ms * 1e-3) / 1e12
+    res = {
+        "what": "token embedding + PreLookaheadLayer + repeat to Mel rows (3 kernels, fp32)",
+        "requests": len(n_tok), "tokens": tokens_total,
+        "ms_per_call": round(ms, 4),
+        "tokens_per_s": round(tokens_total / (ms * 1e-3), 1),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4),
+                     "flop_per_token": flop_per_token,
+                     "timing": f"HIP events around {FRONTEND_REPEAT} back-to-back calls"},
+    }
+    if cpu:
+        from oracle import frontend_oracle as FO
+        torch.set_num_threads(1)
+        empty = [torch.zeros(1, 0, dims.feat)] * len(n_tok)
+        t0 = time.perf_counter()
+        FO.flow_inputs(sd, token_list, empty, torch.ones(len(n_tok), dims.spk_dim))
+        cpu_s = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(tokens_total / cpu_s, 1), "unit": "tokens/s",
+                               "cores": 1, "kind": "port",
+                               "sample": "the same requests through the fp32 oracle front-end "
+                                         "(padded batch, torch CPU conv1d)"}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -132,6 +191,7 @@ def main() -> int:
     ap.add_argument("--workload", type=int, default=3, choices=[2, 3, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
+    ap.add_argument("--no-frontend", action="store_true", help="skip the flow front-end leg")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one (no hipGraph)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration)")
@@ -235,6 +295,11 @@ def main() -> int:
             if vals:
                 breakdown[name] = round(sum(vals) / len(vals), 4)
 
+    frontend = None
+    if not args.no_frontend:
+        log("[bench] flow front-end (tokens -> packed mu rows)")
+        frontend = frontend_leg(fcv, batch, dev, cpu=not args.no_cpu_baseline)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (fp32 oracle, padded SDPA)")
@@ -286,6 +351,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "stage_ms": breakdown,
+        "frontend": frontend,
         "eager_ms_per_step": round(eager_wall * 1e3 / K, 4),
     }
     print(json.dumps(out), flush=True)

@@ -6,11 +6,16 @@ Public surface (mirrors faster_cosyvoice.token2wav.flashinfer_dit / flashinfer_f
   solve_euler_packed      -- packed CFG Euler solve, optionally one hipGraph
   solve_euler_batched     -- padded drop-in of the reference solver
   apply_mi355x            -- install into a Token2Wav flow (apply_flashinfer counterpart)
+  FlowFrontEnd            -- tokens / prompt Mel / x-vectors -> packed mu, cond, spks
+  flow_inference_batched, flow_inference_batched_streaming
+                          -- the flow entry points, front-end through packed solve
 """
 
 from .estimator import DiTEstimator, rope_tables
+from .frontend import FlowFrontEnd, flow_inference_batched, flow_inference_batched_streaming
 from .solver import apply_mi355x, euler_schedule, solve_euler_batched, solve_euler_packed
 from . import synthetic
 
-__all__ = ["DiTEstimator", "apply_mi355x", "euler_schedule", "rope_tables",
+__all__ = ["DiTEstimator", "FlowFrontEnd", "apply_mi355x", "euler_schedule",
+           "flow_inference_batched", "flow_inference_batched_streaming", "rope_tables",
            "solve_euler_batched", "solve_euler_packed", "synthetic"]

@@ -1,4 +1,4 @@
-"""ctypes bindings of libfcvdit.so (declared in include/fcv_dit.h).
+"""ctypes bindings of libfcvdit.so (declared in include/fcv_dit.h and include/fcv_flow.h).
 
 The library is the only compute path: if it is missing, importing the estimator raises,
 there is no fallback.  Error codes map to the exceptions the reference raises for the same
@@ -35,6 +35,19 @@ class FcvDitWeights(ctypes.Structure):
     _fields_ = [(name, c_void_p) for name in WEIGHT_FIELDS]
 
 
+FLOW_MAX_DOCS = 256  # FCV_FLOW_MAX_DOCS
+FLOW_DIM_FIELDS = ("vocab", "feat_dim", "channels", "lookahead", "token_mel_ratio", "spk_dim")
+FLOW_WEIGHT_FIELDS = ("embed", "la1_w", "la1_b", "la2_w", "la2_b", "spk_w", "spk_b")
+
+
+class FcvFlowDims(ctypes.Structure):
+    _fields_ = [(name, c_int32) for name in FLOW_DIM_FIELDS]
+
+
+class FcvFlowWeights(ctypes.Structure):
+    _fields_ = [(name, c_void_p) for name in FLOW_WEIGHT_FIELDS]
+
+
 # (name, restype, argtypes) of every exported entry point
 SIGNATURES = {
     "fcv_last_error": (ctypes.c_char_p, []),
@@ -57,6 +70,15 @@ SIGNATURES = {
                                     c_void_p]),
     "fcv_dit_probe_arm": (c_int32, [c_void_p, c_int32, c_int32, c_int32]),
     "fcv_dit_probe_read": (c_int32, [c_void_p, POINTER(c_float), c_int32, POINTER(c_int32)]),
+    # include/fcv_flow.h
+    "fcv_flow_workspace_bytes": (c_size_t, [POINTER(FcvFlowDims), c_int32]),
+    "fcv_flow_token_features": (c_int32, [POINTER(FcvFlowDims), POINTER(FcvFlowWeights), c_void_p,
+                                          POINTER(c_int32), POINTER(c_int32), c_int32, c_void_p,
+                                          c_void_p, c_size_t, c_void_p]),
+    "fcv_flow_speaker": (c_int32, [POINTER(FcvFlowDims), POINTER(FcvFlowWeights), c_void_p,
+                                   c_int32, c_void_p, c_void_p]),
+    "fcv_flow_prompt_cond": (c_int32, [POINTER(FcvFlowDims), c_void_p, POINTER(c_int32),
+                                       POINTER(c_int32), c_int32, c_void_p, c_void_p]),
 }
 
 STAGES = ("qkv", "attention", "out_proj", "ff1", "ff2", "ln_mod", "conv", "adaln", "in_proj",

@@ -19,7 +19,8 @@ INCLUDE = PKG_DIR.parent / "include"
 LIB_NAME = "libfcvdit.so"
 ARCH = "gfx950"
 
-SOURCES = ["gemm.hip", "gemv.hip", "attention.hip", "conv.hip", "elementwise.hip", "capi.hip"]
+SOURCES = ["gemm.hip", "gemv.hip", "attention.hip", "conv.hip", "elementwise.hip", "frontend.hip",
+           "capi.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

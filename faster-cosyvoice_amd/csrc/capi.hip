@@ -7,6 +7,7 @@
 
 #include "../../include/fcv_dit.h"
 #include "kernels.hpp"
+#include "status.hpp"
 
 using fcv::bf16;
 
@@ -14,22 +15,16 @@ namespace {
 
 thread_local std::string g_error;
 
-int fail(int code, const std::string& msg) {
+}  // namespace
+
+int fcv::fail(int code, const std::string& msg) {
   g_error = msg;
   return code;
 }
 
-#define FCV_HIP(expr)                                                                    \
-  do {                                                                                   \
-    hipError_t e_ = (expr);                                                              \
-    if (e_ != hipSuccess)                                                                \
-      return fail(FCV_ERR_RUNTIME, std::string(#expr) + ": " + hipGetErrorString(e_));   \
-  } while (0)
+using fcv::fail;
 
-#define FCV_CHECK(cond, code, msg)        \
-  do {                                    \
-    if (!(cond)) return fail(code, msg);  \
-  } while (0)
+namespace {
 
 constexpr size_t kAlign = 256;
 constexpr int kMaxSteps = 64;

@@ -110,6 +110,52 @@ def random_state_dict(dims: DiTDims = DiTDims(), seed: int = 0, std: float = 0.0
 
 
 # --------------------------------------------------------------------------
+# Flow front-end (token embedding, PreLookaheadLayer, speaker projection)
+
+
+@dataclass(frozen=True)
+class FlowDims:
+    """Front-end shapes of ``CausalMaskedDiffWithDiT`` (builders.py:29-35)."""
+
+    vocab: int = 6561
+    feat: int = MEL
+    channels: int = 1024
+    lookahead: int = 3
+    spk_dim: int = 192
+    token_mel_ratio: int = 2
+
+
+def flow_state_dict_shapes(d: FlowDims = FlowDims()) -> list[tuple[str, tuple[int, ...]]]:
+    """Front-end parameter names and shapes as they sit in a flow state dict
+    (flow.py:307-310, upsample_encoder.py:61-70)."""
+    return [
+        ("input_embedding.weight", (d.vocab, d.feat)),
+        ("spk_embed_affine_layer.weight", (d.feat, d.spk_dim)),
+        ("spk_embed_affine_layer.bias", (d.feat,)),
+        ("pre_lookahead_layer.conv1.weight", (d.channels, d.feat, d.lookahead + 1)),
+        ("pre_lookahead_layer.conv1.bias", (d.channels,)),
+        ("pre_lookahead_layer.conv2.weight", (d.feat, d.channels, 3)),
+        ("pre_lookahead_layer.conv2.bias", (d.feat,)),
+    ]
+
+
+def random_flow_state_dict(dims: FlowDims = FlowDims(), seed: int = 0) -> dict[str, torch.Tensor]:
+    """Embedding rows ~ N(0, 1) (nn.Embedding's init); every other parameter ~ N(0, 1/fan_in),
+    fan_in = input width of the layer the parameter belongs to, so activations stay O(1).
+    Drawn in ``flow_state_dict_shapes`` order from one PCG64 stream."""
+    fan_in = {"input_embedding": 1, "spk_embed_affine_layer": dims.spk_dim,
+              "pre_lookahead_layer.conv1": dims.feat * (dims.lookahead + 1),
+              "pre_lookahead_layer.conv2": dims.channels * 3}
+    rng = np.random.Generator(np.random.PCG64(seed))
+    sd = {}
+    for name, shape in flow_state_dict_shapes(dims):
+        std = np.float32(1.0 / np.sqrt(fan_in[name.rsplit(".", 1)[0]]))
+        arr = rng.standard_normal(int(np.prod(shape)), dtype=np.float32) * std
+        sd[name] = torch.from_numpy(arr.reshape(shape))
+    return sd
+
+
+# --------------------------------------------------------------------------
 # packed workloads
 
 

@@ -6,5 +6,7 @@ TEST INFRASTRUCTURE ONLY.  Nothing in the product imports this package: only
 never as the thing measured or shipped.
 
 ``dit_oracle`` restates the reference's fp32 torch DiT (padded SDPA with
-boolean masks) and its packed CFG Euler solver.
+boolean masks) and its packed CFG Euler solver; ``frontend_oracle`` restates the
+Flow front-end that produces the DiT inputs (token embedding, PreLookaheadLayer,
+speaker projection, prompt condition).
 """

@@ -12,11 +12,11 @@ import torch
 
 from oracle import dit_oracle as O
 
-HEADER = Path(__file__).resolve().parent.parent / "include" / "fcv_dit.h"
+HEADERS = sorted((Path(__file__).resolve().parent.parent / "include").glob("*.h"))
 
 
 def _declared():
-    text = HEADER.read_text()
+    text = "".join(h.read_text() for h in HEADERS)
     return sorted(set(re.findall(r"\b(fcv_\w+)\s*\(", text)))
 
 
@@ -47,10 +47,14 @@ def test_struct_layouts(fcv):
     from faster_cosyvoice_amd import _lib
     assert ctypes.sizeof(_lib.FcvDitDims) == 10 * 4
     assert ctypes.sizeof(_lib.FcvDitWeights) == 24 * ctypes.sizeof(ctypes.c_void_p)
-    text = HEADER.read_text()
+    text = "".join(h.read_text() for h in HEADERS)
     body = text[text.index("typedef struct FcvDitWeights"):text.index("} FcvDitWeights;")]
     names = re.findall(r"\*\s*(\w+);", body)
     assert tuple(names) == _lib.WEIGHT_FIELDS
+    body = text[text.index("typedef struct FcvFlowDims"):text.index("} FcvFlowDims;")]
+    assert tuple(re.findall(r"int32_t\s+(\w+);", body)) == _lib.FLOW_DIM_FIELDS
+    body = text[text.index("typedef struct FcvFlowWeights"):text.index("} FcvFlowWeights;")]
+    assert tuple(re.findall(r"\*\s*(\w+);", body)) == _lib.FLOW_WEIGHT_FIELDS
 
 
 def _dims(_lib, **kw):
