@@ -17,12 +17,6 @@ here and are replaced by stubs registered in ``sys.modules`` before the import:
   the interleaved-pair rotation (the same arithmetic as the reference's Triton restatement,
   flashinfer_kernels.py:219-249).  The fixtures therefore pin everything except the
   x_transformers rotary arithmetic itself.
-
-``frontend.npz`` pins the Flow front-end's ``PreLookaheadLayer``
-(``cosyvoice/transformer/upsample_encoder.py:55-92``, imported as it is; it needs only torch):
-a padded batch of three token-embedded documents, the same documents one at a time, and one
-call with a right lookahead context (the streaming form, ``flashinfer_flow.py:199-203``).
-``--only frontend`` writes just that file.
 """
 
 from __future__ import annotations
@@ -106,53 +100,12 @@ def _inputs(rng, B, T, lengths):
     return dict(x=x, mu=mu, cond=cond, spks=spks, t=t, mask=mask)
 
 
-def frontend_golden() -> None:
-    """PreLookaheadLayer(80 -> 256 -> 80, lookahead 3) on seeded token embeddings."""
-    from faster_cosyvoice.token2wav.cosyvoice.transformer.upsample_encoder import (  # noqa: E402
-        PreLookaheadLayer)
-
-    syn = _synthetic()
-    torch.set_grad_enabled(False)
-    dims = syn.FlowDims(vocab=97, channels=256)
-    sd = syn.random_flow_state_dict(dims, seed=21)
-    layer = PreLookaheadLayer(in_channels=80, channels=256, pre_lookahead_len=3)
-    layer.load_state_dict({k.split(".", 1)[1]: v for k, v in sd.items()
-                           if k.startswith("pre_lookahead_layer.")})
-    layer.eval()
-    rng = np.random.Generator(np.random.PCG64(4242))
-    lengths = [13, 6, 1]
-    tokens = np.zeros((3, 13), np.int64)
-    for b, n in enumerate(lengths):
-        tokens[b, :n] = rng.integers(0, dims.vocab, size=n)
-    # the offline front-end's masked embedding (flashinfer_flow.py:148-149)
-    emb = sd["input_embedding.weight"][torch.from_numpy(tokens)]
-    mask = torch.zeros(3, 13, 1)
-    for b, n in enumerate(lengths):
-        mask[b, :n] = 1
-    x = emb * mask
-    out_batch = layer(x)
-    out_single = np.zeros((3, 13, 80), np.float32)
-    for b, n in enumerate(lengths):
-        out_single[b, :n] = layer(x[b:b + 1, :n])[0].numpy()
-    ctx_out = layer(x[0:1, :10], context=x[0:1, 10:13])
-    np.savez_compressed(
-        HERE / "frontend.npz", tokens=tokens, lengths=np.array(lengths, np.int32),
-        weight_seed=np.int32(21), vocab=np.int32(dims.vocab), channels=np.int32(dims.channels),
-        x=x.numpy(), out_batch=out_batch.numpy(), out_single=out_single,
-        ctx_split=np.int32(10), ctx_out=ctx_out.numpy())
-
-
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", default="/root/reference")
-    ap.add_argument("--only", choices=["frontend"], default=None)
     args = ap.parse_args()
     _install_stubs()
     sys.path.insert(0, args.ref)
-    frontend_golden()
-    if args.only == "frontend":
-        print("wrote frontend.npz")
-        return
     from faster_cosyvoice.token2wav.cosyvoice.flow.DiT.dit import DiT  # noqa: E402
     from faster_cosyvoice.token2wav.flashinfer_flow import solve_euler_batched  # noqa: E402
 
