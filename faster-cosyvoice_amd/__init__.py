@@ -11,15 +11,17 @@ Public surface (mirrors faster_cosyvoice.token2wav.flashinfer_dit / flashinfer_f
                           -- the flow entry points, front-end through packed solve
   StreamingFlow, CFMDecoder
                           -- stream_step / stream_step_batched (Flow half) over the packed path
+  load_flow               -- the MI355X flow from a flow.pt state dict
 """
 
 from .estimator import DiTEstimator, rope_tables
 from .frontend import FlowFrontEnd, flow_inference_batched, flow_inference_batched_streaming
 from .solver import apply_mi355x, euler_schedule, solve_euler_batched, solve_euler_packed
 from .streaming import CFMDecoder, StreamingFlow
+from .checkpoint import load_flow
 from . import synthetic
 
 __all__ = ["CFMDecoder", "DiTEstimator", "FlowFrontEnd", "StreamingFlow", "apply_mi355x",
            "euler_schedule",
-           "flow_inference_batched", "flow_inference_batched_streaming", "rope_tables",
+           "flow_inference_batched", "flow_inference_batched_streaming", "load_flow", "rope_tables",
            "solve_euler_batched", "solve_euler_packed", "synthetic"]
