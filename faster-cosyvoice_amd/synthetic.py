@@ -156,6 +156,146 @@ def random_flow_state_dict(dims: FlowDims = FlowDims(), seed: int = 0) -> dict[s
 
 
 # --------------------------------------------------------------------------
+# HiFT vocoder (CausalHiFTGenerator + CausalConvRNNF0Predictor)
+
+
+@dataclass(frozen=True)
+class HiFTDims:
+    """Shape of the CosyVoice3 HiFT vocoder (builders.py:38-50)."""
+
+    in_channels: int = MEL
+    base_channels: int = 512
+    nb_harmonics: int = 8
+    sampling_rate: int = 24000
+    nsf_alpha: float = 0.1
+    nsf_sigma: float = 0.003
+    nsf_voiced_threshold: float = 10.0
+    upsample_rates: tuple = (8, 5, 3)
+    upsample_kernel_sizes: tuple = (16, 11, 7)
+    n_fft: int = 16
+    hop_len: int = 4
+    resblock_kernel_sizes: tuple = (3, 7, 11)
+    resblock_dilation_sizes: tuple = ((1, 3, 5), (1, 3, 5), (1, 3, 5))
+    source_resblock_kernel_sizes: tuple = (7, 7, 11)
+    source_resblock_dilation_sizes: tuple = ((1, 3, 5), (1, 3, 5), (1, 3, 5))
+    lrelu_slope: float = 0.1
+    audio_limit: float = 0.99
+    conv_pre_look_right: int = 4
+    f0_channels: int = 512
+
+    @property
+    def upsample_scale(self) -> int:
+        """Waveform samples per Mel frame (prod(upsample_rates) * hop_len)."""
+        out = self.hop_len
+        for r in self.upsample_rates:
+            out *= r
+        return out
+
+    def stage_channels(self, i: int) -> int:
+        return self.base_channels // (2 ** (i + 1))
+
+    def source_down(self, i: int) -> tuple[int, int]:
+        """(kernel, stride) of source_downs[i]: the STFT frames of the source, brought to the
+        rate of upsampling stage i (generator.py:640-655)."""
+        rates = [1] + list(self.upsample_rates[::-1][:-1])
+        cum = list(np.cumprod(rates))[::-1]
+        u = int(cum[i])
+        return (1, 1) if u == 1 else (2 * u, u)
+
+
+def _wn(name: str, shape: tuple[int, ...]) -> list[tuple[str, tuple[int, ...]]]:
+    """A weight-normalised conv: parametrizations g [out,1,1], v [out,in,k], then bias."""
+    return [(f"{name}.parametrizations.weight.original0", (shape[0], 1, 1)),
+            (f"{name}.parametrizations.weight.original1", shape),
+            (f"{name}.bias", (shape[0],))]
+
+
+def _resblock_shapes(name: str, ch: int, k: int, dils) -> list[tuple[str, tuple[int, ...]]]:
+    out = []
+    for j in range(len(dils)):
+        out += _wn(f"{name}.convs1.{j}", (ch, ch, k))
+    for j in range(len(dils)):
+        out += _wn(f"{name}.convs2.{j}", (ch, ch, k))
+    out += [(f"{name}.activations1.{j}.alpha", (ch,)) for j in range(len(dils))]
+    out += [(f"{name}.activations2.{j}.alpha", (ch,)) for j in range(len(dils))]
+    return out
+
+
+def hift_state_dict_shapes(d: HiFTDims = HiFTDims()) -> list[tuple[str, tuple[int, ...]]]:
+    """Parameter names and shapes of ``CausalHiFTGenerator`` in registration order
+    (generator.py:578-675, f0_predictor.py:59-90), as ``hift.pt`` stores them once the
+    ``generator.`` prefix is removed (token2wav.py:71-74)."""
+    H = d.nb_harmonics + 1
+    spec = d.n_fft + 2
+    out = [("m_source.l_linear.weight", (1, H)), ("m_source.l_linear.bias", (1,))]
+    out += _wn("conv_pre", (d.base_channels, d.in_channels, d.conv_pre_look_right + 1))
+    for i, k in enumerate(d.upsample_kernel_sizes):
+        out += _wn(f"ups.{i}", (d.stage_channels(i), d.base_channels // (2 ** i), k))
+    for i in range(len(d.upsample_rates)):
+        k, _ = d.source_down(i)
+        out += [(f"source_downs.{i}.weight", (d.stage_channels(i), spec, k)),
+                (f"source_downs.{i}.bias", (d.stage_channels(i),))]
+    for i, (k, dil) in enumerate(zip(d.source_resblock_kernel_sizes,
+                                     d.source_resblock_dilation_sizes)):
+        out += _resblock_shapes(f"source_resblocks.{i}", d.stage_channels(i), k, dil)
+    n = 0
+    for i in range(len(d.upsample_rates)):
+        for k, dil in zip(d.resblock_kernel_sizes, d.resblock_dilation_sizes):
+            out += _resblock_shapes(f"resblocks.{n}", d.stage_channels(i), k, dil)
+            n += 1
+    out += _wn("conv_post", (spec, d.stage_channels(len(d.upsample_rates) - 1), 7))
+    C = d.f0_channels
+    out += _wn("f0_predictor.condnet.0", (C, d.in_channels, 4))
+    for i in (2, 4, 6, 8):
+        out += _wn(f"f0_predictor.condnet.{i}", (C, C, 3))
+    out += [("f0_predictor.classifier.weight", (1, C)), ("f0_predictor.classifier.bias", (1,))]
+    return out
+
+
+def random_hift_state_dict(dims: HiFTDims = HiFTDims(), seed: int = 0,
+                           post_gain: float = 0.3) -> dict[str, torch.Tensor]:
+    """Seeded HiFT parameters with O(1) activations: weight-norm directions v ~ N(0, 1),
+    gains g ~ N(1, 0.1) (so each conv keeps the variance of its input), biases and the source
+    merge ~ N(0, 0.1), Snake alphas ~ U(0.5, 1.5); ``post_gain`` scales conv_post's gains so
+    the log-magnitudes stay near 0 and the waveform is not clamped.  The F0 head gets weights
+    ~ N(0, 2) and a bias of 10 Hz, so F0 = |10 + O(5)| Hz straddles the 10 Hz voicing threshold
+    and both the voiced and the unvoiced source branches are exercised."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    sd = {}
+    for name, shape in hift_state_dict_shapes(dims):
+        n = int(np.prod(shape))
+        if name.endswith("original0"):
+            arr = 1.0 + 0.1 * rng.standard_normal(n, dtype=np.float32)
+            if name.startswith("conv_post"):
+                arr *= np.float32(post_gain)
+        elif name.endswith("alpha"):
+            arr = rng.uniform(0.5, 1.5, n).astype(np.float32)
+        elif name.endswith("original1"):
+            arr = rng.standard_normal(n, dtype=np.float32)
+        elif name.startswith("source_downs") and name.endswith("weight"):
+            arr = rng.standard_normal(n, dtype=np.float32) / np.float32(np.sqrt(n / shape[0]))
+        else:
+            arr = np.float32(0.1) * rng.standard_normal(n, dtype=np.float32)
+        sd[name] = torch.from_numpy(arr.reshape(shape).astype(np.float32))
+    sd["f0_predictor.classifier.weight"] = sd["f0_predictor.classifier.weight"] * 20.0
+    sd["f0_predictor.classifier.bias"] = torch.full((1,), 10.0)
+    return sd
+
+
+def random_hift_buffers(dims: HiFTDims = HiFTDims(), max_samples: int = 300 * 24000,
+                        seed: int = 0) -> dict[str, torch.Tensor]:
+    """The causal source's fixed random buffers (generator.py:223-226): initial harmonic
+    phases ``rand_ini`` [1, H] with the fundamental's set to 0, and the uniform noise table
+    ``sine_waves`` [1, max_samples, H].  The reference draws them from the global generator
+    when the module is built; pass the reference's own buffers for sample-exact output."""
+    g = torch.Generator().manual_seed(seed)
+    H = dims.nb_harmonics + 1
+    rand_ini = torch.rand(1, H, generator=g)
+    rand_ini[:, 0] = 0
+    return {"rand_ini": rand_ini, "sine_waves": torch.rand(1, max_samples, H, generator=g)}
+
+
+# --------------------------------------------------------------------------
 # packed workloads
 
 

@@ -17,6 +17,14 @@ here and are replaced by stubs registered in ``sys.modules`` before the import:
   the interleaved-pair rotation (the same arithmetic as the reference's Triton restatement,
   flashinfer_kernels.py:219-249).  The fixtures therefore pin everything except the
   x_transformers rotary arithmetic itself.
+
+``hift_small.npz`` pins the wiring of the reference's ``CausalHiFTGenerator.inference``
+(hifigan/generator.py:578-735 with f0_predictor.py:62-103): the order of the upsampling
+stages, the source fusion, the resblock mean, the reflection pad and the two LeakyReLU slopes
+are not fixed by any closed form.  The generator is built at a reduced width (base 32, two
+stages) from its own source; our seeded weights are loaded into it with ``strict=True`` (which
+also pins the ``hift.pt`` parameter names), and its fixed random buffers are stored with the
+outputs.  ``--only hift`` writes just that file.
 """
 
 from __future__ import annotations
@@ -100,12 +108,68 @@ def _inputs(rng, B, T, lengths):
     return dict(x=x, mu=mu, cond=cond, spks=spks, t=t, mask=mask)
 
 
+HIFT_SMALL = dict(base_channels=32, upsample_rates=(2, 3), upsample_kernel_sizes=(4, 5),
+                  resblock_kernel_sizes=(3, 5), resblock_dilation_sizes=((1, 2), (1, 3)),
+                  source_resblock_kernel_sizes=(3, 5), source_resblock_dilation_sizes=((1, 2), (1, 2)),
+                  f0_channels=16)
+
+
+def hift_golden() -> None:
+    """A reduced-width CausalHiFTGenerator on seeded Mel, finalize True and False."""
+    from faster_cosyvoice.token2wav.cosyvoice.hifigan.f0_predictor import (  # noqa: E402
+        CausalConvRNNF0Predictor)
+    from faster_cosyvoice.token2wav.cosyvoice.hifigan.generator import (  # noqa: E402
+        CausalHiFTGenerator)
+
+    syn = _synthetic()
+    torch.set_grad_enabled(False)
+    dims = syn.HiFTDims(**HIFT_SMALL)
+    sd = syn.random_hift_state_dict(dims, seed=61)
+    torch.manual_seed(62)  # the generator draws its fixed source buffers at construction
+    model = CausalHiFTGenerator(
+        in_channels=80, base_channels=dims.base_channels, nb_harmonics=dims.nb_harmonics,
+        sampling_rate=dims.sampling_rate, nsf_alpha=dims.nsf_alpha, nsf_sigma=dims.nsf_sigma,
+        nsf_voiced_threshold=dims.nsf_voiced_threshold,
+        upsample_rates=list(dims.upsample_rates),
+        upsample_kernel_sizes=list(dims.upsample_kernel_sizes),
+        istft_params={"n_fft": dims.n_fft, "hop_len": dims.hop_len},
+        resblock_kernel_sizes=list(dims.resblock_kernel_sizes),
+        resblock_dilation_sizes=[list(d) for d in dims.resblock_dilation_sizes],
+        source_resblock_kernel_sizes=list(dims.source_resblock_kernel_sizes),
+        source_resblock_dilation_sizes=[list(d) for d in dims.source_resblock_dilation_sizes],
+        lrelu_slope=dims.lrelu_slope, audio_limit=dims.audio_limit,
+        conv_pre_look_right=dims.conv_pre_look_right,
+        f0_predictor=CausalConvRNNF0Predictor(num_class=1, in_channels=80,
+                                              cond_channels=dims.f0_channels))
+    model.load_state_dict(sd, strict=True)
+    model.eval()
+    rng = np.random.Generator(np.random.PCG64(63))
+    T = 24
+    mel = torch.from_numpy(rng.standard_normal((1, 80, T)).astype(np.float32))
+    out = {}
+    for fin in (True, False):
+        f0 = model.f0_predictor.to(torch.float64)(mel.double(), finalize=fin)
+        speech, s = model.inference(speech_feat=mel, finalize=fin)
+        tag = "fin" if fin else "stream"
+        out.update({f"f0_{tag}": f0.numpy(), f"speech_{tag}": speech.numpy(), f"s_{tag}": s.numpy()})
+    L = T * dims.upsample_scale
+    gen = model.m_source.l_sin_gen
+    np.savez_compressed(
+        HERE / "hift_small.npz", mel=mel.numpy(), weight_seed=np.int32(61),
+        rand_ini=gen.rand_ini.numpy(), sine_waves=gen.sine_waves[:, :L].numpy(), **out)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", default="/root/reference")
+    ap.add_argument("--only", choices=["hift"], default=None)
     args = ap.parse_args()
     _install_stubs()
     sys.path.insert(0, args.ref)
+    if args.only == "hift":
+        hift_golden()
+        print("wrote hift_small.npz")
+        return
     from faster_cosyvoice.token2wav.cosyvoice.flow.DiT.dit import DiT  # noqa: E402
     from faster_cosyvoice.token2wav.flashinfer_flow import solve_euler_batched  # noqa: E402
 
@@ -155,6 +219,7 @@ def main() -> None:
         HERE / "block1024.npz", **inp, lengths=np.array([64], np.int32), chunk=np.int32(50),
         weight_seed=np.int32(5), gate_bias=np.float32(0.5), dim=np.int32(1024), depth=np.int32(1),
         heads=np.int32(16), out_full=out_full.numpy(), out_stream=out_stream.numpy())
+    hift_golden()
     print("wrote", sorted(p.name for p in HERE.glob("*.npz")))
 
 
