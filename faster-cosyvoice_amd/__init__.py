@@ -12,6 +12,7 @@ Public surface (mirrors faster_cosyvoice.token2wav.flashinfer_dit / flashinfer_f
   StreamingFlow, CFMDecoder
                           -- stream_step / stream_step_batched (Flow half) over the packed path
   load_flow               -- the MI355X flow from a flow.pt state dict
+  HiFTVocoder             -- the HiFT vocoder (CausalHiFTGenerator counterpart), packed batches
 """
 
 from .estimator import DiTEstimator, rope_tables
@@ -19,9 +20,11 @@ from .frontend import FlowFrontEnd, flow_inference_batched, flow_inference_batch
 from .solver import apply_mi355x, euler_schedule, solve_euler_batched, solve_euler_packed
 from .streaming import CFMDecoder, StreamingFlow
 from .checkpoint import load_flow
+from .hift import HiFTVocoder
 from . import synthetic
 
-__all__ = ["CFMDecoder", "DiTEstimator", "FlowFrontEnd", "StreamingFlow", "apply_mi355x",
+__all__ = ["CFMDecoder", "DiTEstimator", "FlowFrontEnd", "HiFTVocoder", "StreamingFlow",
+           "apply_mi355x",
            "euler_schedule",
            "flow_inference_batched", "flow_inference_batched_streaming", "load_flow", "rope_tables",
            "solve_euler_batched", "solve_euler_packed", "synthetic"]

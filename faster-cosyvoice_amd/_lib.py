@@ -1,4 +1,4 @@
-"""ctypes bindings of libfcvdit.so (declared in include/fcv_dit.h and include/fcv_flow.h).
+"""ctypes bindings of libfcvdit.so (declared in include/fcv_dit.h, fcv_flow.h and fcv_hift.h).
 
 The library is the only compute path: if it is missing, importing the estimator raises,
 there is no fallback.  Error codes map to the exceptions the reference raises for the same
@@ -48,6 +48,24 @@ class FcvFlowWeights(ctypes.Structure):
     _fields_ = [(name, c_void_p) for name in FLOW_WEIGHT_FIELDS]
 
 
+HIFT_MAX = 4          # FCV_HIFT_MAX
+HIFT_MAX_DOCS = 256   # FCV_HIFT_MAX_DOCS
+_I4 = c_int32 * HIFT_MAX
+
+
+class FcvHiftDims(ctypes.Structure):
+    _fields_ = [
+        ("in_channels", c_int32), ("base_channels", c_int32), ("nb_harmonics", c_int32),
+        ("sampling_rate", c_int32), ("nsf_alpha", c_float), ("nsf_sigma", c_float),
+        ("nsf_voiced_threshold", c_float), ("n_stages", c_int32), ("upsample_rates", _I4),
+        ("upsample_kernels", _I4), ("n_kernels", c_int32), ("resblock_kernels", _I4),
+        ("n_dilations", c_int32), ("resblock_dilations", _I4 * HIFT_MAX),
+        ("source_kernels", _I4), ("source_dilations", _I4 * HIFT_MAX), ("n_fft", c_int32),
+        ("hop_len", c_int32), ("conv_pre_look_right", c_int32), ("f0_channels", c_int32),
+        ("lrelu_slope", c_float), ("audio_limit", c_float), ("noise_samples", c_int32),
+    ]
+
+
 # (name, restype, argtypes) of every exported entry point
 SIGNATURES = {
     "fcv_last_error": (ctypes.c_char_p, []),
@@ -79,6 +97,17 @@ SIGNATURES = {
                                    c_int32, c_void_p, c_void_p]),
     "fcv_flow_prompt_cond": (c_int32, [POINTER(FcvFlowDims), c_void_p, POINTER(c_int32),
                                        POINTER(c_int32), c_int32, c_void_p, c_void_p]),
+    # include/fcv_hift.h
+    "fcv_hift_weight_count": (c_int32, [POINTER(FcvHiftDims)]),
+    "fcv_hift_create": (c_int32, [POINTER(FcvHiftDims), POINTER(c_void_p), c_int32,
+                                  POINTER(c_void_p)]),
+    "fcv_hift_destroy": (c_int32, [c_void_p]),
+    "fcv_hift_output_samples": (ctypes.c_int64, [c_void_p, c_int32, c_int32]),
+    "fcv_hift_workspace_bytes": (c_size_t, [c_void_p, POINTER(c_int32), POINTER(c_int32),
+                                            c_int32]),
+    "fcv_hift_inference": (c_int32, [c_void_p, c_void_p, POINTER(c_int32), POINTER(c_int32),
+                                     c_int32, c_void_p, c_void_p, c_void_p, c_size_t,
+                                     c_void_p]),
 }
 
 STAGES = ("qkv", "attention", "out_proj", "ff1", "ff2", "ln_mod", "conv", "adaln", "in_proj",

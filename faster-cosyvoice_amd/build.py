@@ -20,7 +20,7 @@ LIB_NAME = "libfcvdit.so"
 ARCH = "gfx950"
 
 SOURCES = ["gemm.hip", "gemv.hip", "attention.hip", "conv.hip", "elementwise.hip", "frontend.hip",
-           "capi.hip"]
+           "hift.hip", "hift_capi.hip", "capi.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -1,0 +1,443 @@
+// HiFT vocoder kernels on gfx950 (see hift.hpp for the layout and the launch contracts).
+//
+// Every convolution of the vocoder -- the fp64 F0 predictor, conv_pre, the upsampling convs,
+// the strided source convs, the resblock convs and conv_post -- is one implicit GEMM on the
+// matrix cores (v_mfma_{f32,f64}_16x16x4): weights are the A operand (rows = output channels),
+// the gathered input rows the B operand, so a lane's four accumulators are four channels of one
+// time step (consecutive in fp32; four apart in fp64, whose 16x16 result is laid out by rows
+// 4 e + lane / 16).  Operands go through LDS K-contiguous, 16 input channels of one tap
+// per chunk, with a register-prefetched double buffer.  A workgroup owns 64 time rows x 64
+// output channels.  Activations that sit between two convolutions are fused: LeakyReLU into the
+// input prologue, bias, ELU, residual add, Snake and the resblock mean into the epilogue, and
+// the epilogue can also write Snake(y) as a second output for the next conv.
+#include <math.h>
+
+#include "hift.hpp"
+
+namespace fcv {
+namespace {
+
+constexpr int kBK = 16;     // input channels per chunk
+constexpr int kPitch = 20;  // LDS row pitch in elements
+constexpr int kTileR = 64;  // time rows per workgroup
+constexpr int kTileC = 64;  // output channels per workgroup
+
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Vec4;
+template <> struct Vec4<float> { using type = f32x4; };
+template <> struct Vec4<double> { using type = f64x4; };
+
+__device__ __forceinline__ f32x4 mfma_16x16x4(float a, float b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f64x4 mfma_16x16x4(double a, double b, const f64x4& c) {
+  return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+// largest d with cu[d] <= row
+__device__ __forceinline__ int doc_of(const int32_t* cu, int n_docs, int row) {
+  int lo = 0, hi = n_docs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (cu[mid] <= row) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Snake(x) = x + sin(a x)^2 / (a + 1e-9), with inv = 1 / (a + 1e-9) precomputed in fp32
+__device__ __forceinline__ float snake(float x, float a, float inv) {
+  const float s = sinf(x * a);
+  return x + inv * (s * s);
+}
+
+template <typename T>
+__device__ __forceinline__ T elu(T x) { return x > T(0) ? x : T(expm1(x)); }
+
+// epilogue of one output element (row, channel c) from its accumulator value
+template <typename T>
+__device__ __forceinline__ void conv_store1(const HiftConv& p, long row, int c, T acc) {
+  T v = acc + static_cast<const T*>(p.bias)[c];
+  if constexpr (sizeof(T) == 8) {
+    if (p.elu) v = elu(v);
+  }
+  const long i = row * p.ldo + c;
+  if (p.add) v = v + static_cast<const T*>(p.add)[row * p.ld_add + c];
+  if (p.mode == HIFT_ACC_ADD) v = static_cast<const T*>(p.accin)[i] + v;
+  if (p.mode == HIFT_ACC_ADD_DIV) v = (static_cast<const T*>(p.accin)[i] + v) / T(p.div);
+  if constexpr (sizeof(T) == 4) {
+    if (p.snake_out) v = snake(v, p.alpha[c], p.inv_alpha[c]);
+    if (p.out2) static_cast<float*>(p.out2)[i] = snake(v, p.alpha2[c], p.inv_alpha2[c]);
+  }
+  static_cast<T*>(p.out)[i] = v;
+}
+
+// The 16x16x4 accumulators of lane (li, lg) hold, for the tile's channel base cb:
+//   fp32: channels cb + 4 lg + e;  fp64: channels cb + 4 e + lg  (e = 0..3)
+template <typename T>
+__device__ void conv_store(const HiftConv& p, long row, int cb, int lg,
+                           const typename Vec4<T>::type& acc) {
+  for (int e = 0; e < 4; ++e) {
+    const int c = sizeof(T) == 4 ? cb + 4 * lg + e : cb + 4 * e + lg;
+    if (c < p.cout) conv_store1<T>(p, row, c, acc[e]);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const HiftDocs docs) {
+  using VT = typename Vec4<T>::type;
+  __shared__ __attribute__((aligned(16))) T sA[2][kTileC][kPitch];
+  __shared__ __attribute__((aligned(16))) T sB[2][kTileR][kPitch];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wc = wave & 1, wt = wave >> 1;
+  const int li = lane & 15, lg = lane >> 4;
+  const int r0 = blockIdx.x * kTileR;
+  const int co0 = blockIdx.y * kTileC;
+  const int cpt = p.cin_pad / kBK;
+  const int KC = p.k * cpt;
+  const long kcin = (long)p.k * p.cin_pad;
+
+  // loader roles: weight row lr / input row lr, 4-element quarter lq of the 16-channel chunk
+  const int lr = tid >> 2, lq = tid & 3;
+  const int r = r0 + lr;
+  const bool valid = r < p.rows_out;
+  int in_base = 0, in_len = 0, pos = 0;
+  if (valid) {
+    const int d = doc_of(docs.b, p.n_docs, r);
+    pos = r - docs.b[d];
+    in_base = docs.a[d];
+    in_len = docs.a[d + 1] - in_base;
+  }
+  const T* X = static_cast<const T*>(p.x);
+  const T* W = static_cast<const T*>(p.w) + (long)(co0 + lr) * kcin + 4 * lq;
+
+  VT ra, rb;
+  auto fetch = [&](int kc) {
+    const int tap = kc / cpt;
+    const int c0 = (kc - tap * cpt) * kBK + 4 * lq;
+    ra = *reinterpret_cast<const VT*>(W + (long)kc * kBK);
+    rb = VT{T(0), T(0), T(0), T(0)};
+    const int u = pos * p.stride + tap * p.dil - p.pad;
+    const int q = p.up > 1 ? (u >= 0 ? u / p.up : -1) : u;
+    if (valid && q >= 0 && q < in_len) {
+      rb = *reinterpret_cast<const VT*>(X + (long)(in_base + q) * p.ldx + c0);
+      if constexpr (sizeof(T) == 4) {
+        if (p.pro == HIFT_PRO_LEAKY) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rb[e] = rb[e] > 0.0f ? rb[e] : rb[e] * p.slope;
+        }
+      }
+    }
+  };
+  auto stash = [&](int buf) {
+    *reinterpret_cast<VT*>(&sA[buf][lr][4 * lq]) = ra;
+    *reinterpret_cast<VT*>(&sB[buf][lr][4 * lq]) = rb;
+  };
+
+  VT acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = VT{T(0), T(0), T(0), T(0)};
+
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int kc = 0; kc < KC; ++kc) {
+    const int cur = kc & 1;
+    if (kc + 1 < KC) fetch(kc + 1);
+    VT av[2], bv[2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+      av[a] = *reinterpret_cast<const VT*>(&sA[cur][wc * 32 + a * 16 + li][4 * lg]);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+      bv[b] = *reinterpret_cast<const VT*>(&sB[cur][wt * 32 + b * 16 + li][4 * lg]);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = mfma_16x16x4(av[a][s], bv[b][s], acc[a][b]);
+    if (kc + 1 < KC) stash(cur ^ 1);
+    __syncthreads();
+  }
+
+  // D[i = channel][j = row]: lane holds row li and four channels of each 16x16 tile
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int rr = r0 + wt * 32 + b * 16 + li;
+    if (rr >= p.rows_out) continue;
+    const int d = doc_of(docs.b, p.n_docs, rr);
+    const int pp = rr - docs.b[d];
+    const long row_w = p.reflect ? (long)docs.b[d] + d + 1 + pp : rr;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int cb = co0 + wc * 32 + a * 16;
+      conv_store<T>(p, row_w, cb, lg, acc[a][b]);
+      // reflection padding (1, 0): row 0 of the document repeats the result's row 1
+      if (p.reflect && pp == 1) conv_store<T>(p, (long)docs.b[d] + d, cb, lg, acc[a][b]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void snake_kernel(const float* __restrict__ x, int ldx,
+                                                    float* __restrict__ out, int ldo, int rows,
+                                                    int C, const float* __restrict__ alpha,
+                                                    const float* __restrict__ inv_alpha) {
+  const int q = C / 4;
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)rows * q) return;
+  const long r = i / q;
+  const int c = (int)(i - r * q) * 4;
+  const f32x4 v = *reinterpret_cast<const f32x4*>(x + r * ldx + c);
+  f32x4 y;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) y[e] = snake(v[e], alpha[c + e], inv_alpha[c + e]);
+  *reinterpret_cast<f32x4*>(out + r * ldo + c) = y;
+}
+
+__global__ __launch_bounds__(256) void to_f64_kernel(const float* __restrict__ x,
+                                                     double* __restrict__ y, long n) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (double)x[i];
+}
+
+__global__ __launch_bounds__(64) void f0_head_kernel(const double* __restrict__ h, int C,
+                                                     const double* __restrict__ w,
+                                                     const double* __restrict__ b,
+                                                     float* __restrict__ f0) {
+  const long r = blockIdx.x;
+  double s = 0.0;
+  for (int c = threadIdx.x; c < C; c += 64) s = fma(h[r * C + c], w[c], s);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (threadIdx.x == 0) f0[r] = (float)fabs(s + b[0]);
+}
+
+// One thread per (document, harmonic): the per-frame phase increment of harmonic h is
+// rad = frac(f0 (h+1) / sr); the frame-rate value is the linear interpolation the reference
+// takes from the sample-rate sequence (whose first sample also carries rand_ini[h]); the
+// phase is the running sum in frame order, times 2 pi, times the upsampling scale.
+__global__ __launch_bounds__(64) void source_phase_kernel(const HiftSource p,
+                                                          const HiftDocs docs) {
+#pragma clang fp contract(off)
+  const int d = blockIdx.x;
+  const int h = threadIdx.x;
+  if (h >= p.H) return;
+  const int f_base = docs.a[d];
+  const int T = docs.a[d + 1] - f_base;
+  const long L = (long)T * p.scale;
+  const float mult = (float)(h + 1);
+  const float sr = (float)p.sampling_rate;
+  const float scale = (float)p.scale;
+  auto rad_at = [&](long i) {
+    const float x = (p.f0[f_base + i / p.scale] * mult) / sr;
+    float v = x - floorf(x);
+    if (i == 0) v = v + p.rand_ini[h];
+    return v;
+  };
+  float c = 0.0f;
+  for (int t = 0; t < T; ++t) {
+    float src = scale * ((float)t + 0.5f) - 0.5f;
+    if (src < 0.0f) src = 0.0f;
+    const long i0 = (long)src;
+    const float l1 = fminf(fmaxf(src - (float)i0, 0.0f), 1.0f);
+    const float l0 = 1.0f - l1;
+    const long i1 = i0 + (i0 < L - 1 ? 1 : 0);
+    const float a = l0 * rad_at(i0);
+    const float b = l1 * rad_at(i1);
+    c = c + (a + b);
+    float ph = (c * 2.0f) * 3.14159265358979323846f;
+    ph = ph * scale;
+    p.sines[(long)(f_base + t) * p.H + h] = sinf(ph) * p.sine_amp;
+  }
+}
+
+__global__ __launch_bounds__(256) void source_sample_kernel(const HiftSource p,
+                                                            const HiftDocs docs, int samples) {
+#pragma clang fp contract(off)
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= samples) return;
+  const int d = doc_of(docs.b, p.n_docs, n);
+  const int pos = n - docs.b[d];
+  const int fr = docs.a[d] + pos / p.scale;
+  const float f0 = p.f0[fr];
+  const float uv = f0 > p.voiced_threshold ? 1.0f : 0.0f;
+  const float amp = uv * p.noise_std + ((1.0f - uv) * p.sine_amp) / 3.0f;
+  const float* noise = p.table + (long)pos * p.H;
+  float acc = 0.0f;
+  for (int h = 0; h < p.H; ++h) {
+    const float wave = p.sines[(long)fr * p.H + h] * uv + amp * noise[h];
+    acc = acc + p.lin_w[h] * wave;
+  }
+  p.s[n] = tanhf(acc + p.lin_b[0]);
+}
+
+// cos / sin of 2 pi m / 16 for m = 0..15
+__device__ __forceinline__ float cos16(int m) { return cospif((float)(m & 15) / 8.0f); }
+__device__ __forceinline__ float sin16(int m) { return sinpif((float)(m & 15) / 8.0f); }
+
+__global__ __launch_bounds__(256) void stft_kernel(const float* __restrict__ s,
+                                                   const float* __restrict__ win,
+                                                   float* __restrict__ out, int ld, int n_docs,
+                                                   int frames, const HiftDocs docs) {
+  const int f = blockIdx.x * blockDim.x + threadIdx.x;
+  if (f >= frames) return;
+  const int d = doc_of(docs.b, n_docs, f);
+  const int fl = f - docs.b[d];
+  const float* x = s + docs.a[d];
+  const int L = docs.a[d + 1] - docs.a[d];
+  float v[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    int i = 4 * fl + j - 8;
+    if (i < 0) i = -i;
+    if (i >= L) i = 2 * (L - 1) - i;
+    v[j] = x[i] * win[j];
+  }
+  float* o = out + (long)f * ld;
+#pragma unroll
+  for (int k = 0; k <= 8; ++k) {
+    float re = 0.0f, im = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      re = fmaf(v[j], cos16(j * k), re);
+      im = fmaf(-v[j], sin16(j * k), im);
+    }
+    o[k] = re;
+    o[9 + k] = im;
+  }
+  for (int c = 18; c < ld; ++c) o[c] = 0.0f;
+}
+
+// windowed inverse real DFT of one frame: mag = min(exp(y[k]), 100), ph = sin(y[9 + k])
+__global__ __launch_bounds__(256) void istft_frame_kernel(const float* __restrict__ y, int ldy,
+                                                          const float* __restrict__ win,
+                                                          float* __restrict__ fr, int frames) {
+  const int f = blockIdx.x * blockDim.x + threadIdx.x;
+  if (f >= frames) return;
+  const float* row = y + (long)f * ldy;
+  float re[9], im[9];
+#pragma unroll
+  for (int k = 0; k <= 8; ++k) {
+    const float mag = fminf(expf(row[k]), 100.0f);
+    const float ph = sinf(row[9 + k]);
+    re[k] = mag * cosf(ph);
+    im[k] = mag * sinf(ph);
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    float acc = re[0] + ((j & 1) ? -re[8] : re[8]);
+    float h = 0.0f;
+#pragma unroll
+    for (int k = 1; k <= 7; ++k) h = h + (re[k] * cos16(j * k) - im[k] * sin16(j * k));
+    acc = (acc + 2.0f * h) * (1.0f / 16.0f);
+    fr[(long)f * 16 + j] = acc * win[j];
+  }
+}
+
+// overlap-add: output sample pos of document d sits at padded position pos + 8 of the frame
+// sequence; divided by the overlap-added squared window, clamped
+__global__ __launch_bounds__(256) void istft_ola_kernel(const float* __restrict__ fr,
+                                                        const float* __restrict__ win,
+                                                        float* __restrict__ out, float limit,
+                                                        int n_docs, int samples,
+                                                        const HiftDocs docs) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= samples) return;
+  const int d = doc_of(docs.b, n_docs, n);
+  const int P = n - docs.b[d] + 8;
+  const int f_base = docs.a[d];
+  const int F = docs.a[d + 1] - f_base;
+  float y = 0.0f, env = 0.0f;
+  const int f_hi = min(P / 4, F - 1);
+  for (int f = max(0, (P - 12) / 4); f <= f_hi; ++f) {
+    const int j = P - 4 * f;
+    if (j < 0 || j >= 16) continue;
+    y = y + fr[(long)(f_base + f) * 16 + j];
+    env = env + win[j] * win[j];
+  }
+  const float v = y / env;
+  out[n] = fminf(fmaxf(v, -limit), limit);
+}
+
+unsigned blocks_for(long n, int threads) { return (unsigned)((n + threads - 1) / threads); }
+
+template <typename T>
+hipError_t launch_conv(const HiftConv& p, const HiftDocs& docs, hipStream_t stream) {
+  if (p.rows_out <= 0) return hipSuccess;
+  const dim3 grid((p.rows_out + kTileR - 1) / kTileR, (p.cout + kTileC - 1) / kTileC);
+  hipLaunchKernelGGL(hift_conv_kernel<T>, grid, dim3(256), 0, stream, p, docs);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t hift_conv_f32(const HiftConv& p, const HiftDocs& docs, hipStream_t stream) {
+  return launch_conv<float>(p, docs, stream);
+}
+hipError_t hift_conv_f64(const HiftConv& p, const HiftDocs& docs, hipStream_t stream) {
+  return launch_conv<double>(p, docs, stream);
+}
+
+hipError_t hift_snake(const float* x, int ldx, float* out, int ldo, int rows, int C,
+                      const float* alpha, const float* inv_alpha, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  const long n = (long)rows * (C / 4);
+  hipLaunchKernelGGL(snake_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, x, ldx, out,
+                     ldo, rows, C, alpha, inv_alpha);
+  return hipGetLastError();
+}
+
+hipError_t hift_to_f64(const float* x, double* y, long n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(to_f64_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t hift_f0_head(const double* h, int C, const double* cls_w, const double* cls_b,
+                        int rows, float* f0, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(f0_head_kernel, dim3(rows), dim3(64), 0, stream, h, C, cls_w, cls_b, f0);
+  return hipGetLastError();
+}
+
+hipError_t hift_source(const HiftSource& p, const HiftDocs& docs, hipStream_t stream) {
+  hipLaunchKernelGGL(source_phase_kernel, dim3(p.n_docs), dim3(64), 0, stream, p, docs);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int samples = docs.b[p.n_docs];
+  if (samples <= 0) return hipSuccess;
+  hipLaunchKernelGGL(source_sample_kernel, dim3(blocks_for(samples, 256)), dim3(256), 0, stream,
+                     p, docs, samples);
+  return hipGetLastError();
+}
+
+hipError_t hift_stft(const float* s, const float* window, float* out, int ld, int n_docs,
+                     int frames, const HiftDocs& docs, hipStream_t stream) {
+  if (frames <= 0) return hipSuccess;
+  hipLaunchKernelGGL(stft_kernel, dim3(blocks_for(frames, 256)), dim3(256), 0, stream, s, window,
+                     out, ld, n_docs, frames, docs);
+  return hipGetLastError();
+}
+
+hipError_t hift_istft(const float* y, int ldy, const float* window, float* fr, float* out,
+                      float limit, int n_docs, int frames, int samples, const HiftDocs& docs,
+                      hipStream_t stream) {
+  if (frames > 0) {
+    hipLaunchKernelGGL(istft_frame_kernel, dim3(blocks_for(frames, 256)), dim3(256), 0, stream, y,
+                       ldy, window, fr, frames);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (samples <= 0) return hipSuccess;
+  hipLaunchKernelGGL(istft_ola_kernel, dim3(blocks_for(samples, 256)), dim3(256), 0, stream, fr,
+                     window, out, limit, n_docs, samples, docs);
+  return hipGetLastError();
+}
+
+}  // namespace fcv

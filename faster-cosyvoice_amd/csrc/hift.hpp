@@ -1,0 +1,88 @@
+// Kernels of the HiFT vocoder (hift.hip) and their launch parameters; the orchestration and the
+// C ABI live in hift_capi.hip.  All activations are time-major: row = time step of one
+// document, channels contiguous; documents are packed one after another, and every launch
+// takes the per-document row prefix sums by value (HiftDocs, at most kHiftMaxDocs documents).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.hpp"
+
+namespace fcv {
+
+constexpr int kHiftMaxDocs = 256;
+
+// two exclusive prefix sums over documents: a = input rows, b = output rows
+struct HiftDocs {
+  int32_t a[kHiftMaxDocs + 1];
+  int32_t b[kHiftMaxDocs + 1];
+};
+
+enum { HIFT_PRO_NONE = 0, HIFT_PRO_LEAKY = 1 };
+enum { HIFT_ACC_WRITE = 0, HIFT_ACC_ADD = 1, HIFT_ACC_ADD_DIV = 2 };
+
+// One 1-D convolution as an implicit GEMM: out[r][co] over output rows r of every document.
+// Input position of tap j for output position p of a document:
+//   u = p * stride + j * dil - pad;  q = up > 1 ? (u >= 0 ? u / up : -1) : u
+// and the input row is read when 0 <= q < the document's input length (zero otherwise).
+// Weights are packed [cout rounded up to 64][k][cin_pad] (cin_pad % 16 == 0, zero padding).
+struct HiftConv {
+  const void* x; int ldx;                 // input rows [*][ldx], ldx >= cin_pad
+  const void* w; const void* bias;
+  int cout, cin_pad, k, stride, dil, pad, up;
+  int rows_out, n_docs;
+  int reflect;                             // write row p + 1 (row 0 = row 2 of the result)
+  int pro; float slope;                    // prologue on the inputs (fp32 only)
+  int elu;                                 // epilogue ELU (fp64 only)
+  const void* add; int ld_add;             // y += add[row] (layout of out)
+  int mode; const void* accin; float div;  // y = accin + y  or  (accin + y) / div
+  const float* alpha; const float* inv_alpha;    // snake_out: out = snake(y)
+  int snake_out;
+  void* out; int ldo;
+  void* out2; const float* alpha2; const float* inv_alpha2;  // out2 = snake(y) (optional)
+};
+
+hipError_t hift_conv_f32(const HiftConv& p, const HiftDocs& docs, hipStream_t stream);
+hipError_t hift_conv_f64(const HiftConv& p, const HiftDocs& docs, hipStream_t stream);
+
+// out[r][c] = snake(x[r][c]) for rows x C channels (C % 4 == 0), row strides ldx / ldo
+hipError_t hift_snake(const float* x, int ldx, float* out, int ldo, int rows, int C,
+                      const float* alpha, const float* inv_alpha, hipStream_t stream);
+
+// fp32 -> fp64 rows (C % 4 == 0)
+hipError_t hift_to_f64(const float* x, double* y, long n, hipStream_t stream);
+
+// f0[r] = (float)|cls_w . h[r] + cls_b| (fp64 dot over C channels), one wave per row
+hipError_t hift_f0_head(const double* h, int C, const double* cls_w, const double* cls_b,
+                        int rows, float* f0, hipStream_t stream);
+
+struct HiftSource {
+  const float* f0;          // frame F0, rows by docs.a
+  const float* rand_ini;    // [H]
+  const float* table;       // noise table [max_samples][H]
+  int max_samples;
+  const float* lin_w; const float* lin_b;  // [H], [1]
+  int H, scale, sampling_rate;
+  float sine_amp, noise_std, voiced_threshold;
+  int n_docs;
+  float* sines;             // [frames][H] work: sin(phase) * sine_amp per frame
+  float* s;                 // [samples] source, rows by docs.b
+};
+// per-frame phases (sequential sum per document and harmonic) then per-sample merge
+hipError_t hift_source(const HiftSource& p, const HiftDocs& docs, hipStream_t stream);
+
+// STFT frames (n_fft 16, hop 4, centred, reflect padding) of each document's source:
+// out[f][0..8] = Re, out[f][9..17] = Im, out[f][18..ld) = 0; docs.a = samples, docs.b = frames
+hipError_t hift_stft(const float* s, const float* window, float* out, int ld, int n_docs,
+                     int frames, const HiftDocs& docs, hipStream_t stream);
+
+// iSTFT: per frame f of y [frames][ldy] (log-magnitudes 0..8, phase inputs 9..17), the
+// windowed inverse real DFT into fr [frames][16]; then centred overlap-add divided by the
+// window envelope, clamped to +-limit, keeping the first docs.b lengths of each document.
+// docs.a = frames, docs.b = output samples.
+hipError_t hift_istft(const float* y, int ldy, const float* window, float* fr, float* out,
+                      float limit, int n_docs, int frames, int samples, const HiftDocs& docs,
+                      hipStream_t stream);
+
+}  // namespace fcv

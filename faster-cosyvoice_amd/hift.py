@@ -1,0 +1,251 @@
+"""``HiFTVocoder``: the MI355X drop-in for the reference's ``CausalHiFTGenerator`` (Mel -> 24 kHz
+waveform, hifigan/generator.py:578-735), compute in libfcvdit.so (include/fcv_hift.h).
+
+Holds the reference's parameters under their ``hift.pt`` names (``conv_pre.parametrizations.
+weight.original0`` ...; a ``generator.`` prefix is accepted, token2wav.py:71-74) and the causal
+source's fixed random buffers.  ``finalize_weights`` folds weight norm, packs every conv weight
+as [ceil64(cout)][k][ceil16(cin)], and keeps the F0 predictor in fp64 as the reference does
+(generator.py:722).  ``inference(speech_feat, finalize)`` has the reference's signature;
+``inference_batched`` vocodes several requests of different lengths in one packed call.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+
+import numpy as np
+import torch
+from scipy.signal import get_window
+
+from . import _lib
+from .synthetic import HiFTDims, hift_state_dict_shapes, random_hift_buffers
+
+_G = ".parametrizations.weight.original0"
+_V = ".parametrizations.weight.original1"
+
+
+def _ceil(v: int, m: int) -> int:
+    return (v + m - 1) // m * m
+
+
+class HiFTVocoder:
+    """Packed-batch HiFT vocoder on gfx950 HIP kernels (CausalHiFTGenerator counterpart)."""
+
+    def __init__(self, dims: HiFTDims = HiFTDims(), device: torch.device | str = "cuda:0",
+                 buffers: dict[str, torch.Tensor] | None = None):
+        self.dims = dims
+        self.device = torch.device(device)
+        self.state: dict[str, torch.Tensor] | None = None
+        self.buffers = buffers
+        self._lib = _lib.load()
+        self._cdims = self._make_dims()
+        self._handle: int | None = None
+        self._keep: list[torch.Tensor] = []
+        self._ws: torch.Tensor | None = None
+
+    # ---- construction ----------------------------------------------------------------------
+
+    def _make_dims(self) -> _lib.FcvHiftDims:
+        d = self.dims
+        c = _lib.FcvHiftDims()
+        c.in_channels, c.base_channels, c.nb_harmonics = d.in_channels, d.base_channels, d.nb_harmonics
+        c.sampling_rate = d.sampling_rate
+        c.nsf_alpha, c.nsf_sigma, c.nsf_voiced_threshold = d.nsf_alpha, d.nsf_sigma, d.nsf_voiced_threshold
+        c.n_stages = len(d.upsample_rates)
+        for i, (r, k) in enumerate(zip(d.upsample_rates, d.upsample_kernel_sizes)):
+            c.upsample_rates[i], c.upsample_kernels[i] = r, k
+        c.n_kernels = len(d.resblock_kernel_sizes)
+        c.n_dilations = len(d.resblock_dilation_sizes[0])
+        for j, (k, dil) in enumerate(zip(d.resblock_kernel_sizes, d.resblock_dilation_sizes)):
+            c.resblock_kernels[j] = k
+            for m, v in enumerate(dil):
+                c.resblock_dilations[j][m] = v
+        for i, (k, dil) in enumerate(zip(d.source_resblock_kernel_sizes,
+                                         d.source_resblock_dilation_sizes)):
+            if len(dil) != c.n_dilations:
+                raise ValueError("source and main resblocks must have the same dilation count")
+            c.source_kernels[i] = k
+            for m, v in enumerate(dil):
+                c.source_dilations[i][m] = v
+        c.n_fft, c.hop_len = d.n_fft, d.hop_len
+        c.conv_pre_look_right, c.f0_channels = d.conv_pre_look_right, d.f0_channels
+        c.lrelu_slope, c.audio_limit = d.lrelu_slope, d.audio_limit
+        c.noise_samples = 0
+        return c
+
+    def load_reference_state_dict(self, sd: dict[str, torch.Tensor]) -> None:
+        """Strict load of a ``hift.pt`` state dict (``generator.`` prefix optional)."""
+        sd = {k[len("generator."):] if k.startswith("generator.") else k: v for k, v in sd.items()}
+        want = dict(hift_state_dict_shapes(self.dims))
+        missing = [k for k in want if k not in sd]
+        unexpected = [k for k in sd if k not in want]
+        if missing or unexpected:
+            raise RuntimeError(f"HiFT state-dict mismatch: missing={missing[:8]}, "
+                               f"unexpected={unexpected[:8]}")
+        bad = [k for k, s in want.items() if tuple(sd[k].shape) != tuple(s)]
+        if bad:
+            raise RuntimeError(f"HiFT state-dict shape mismatch: {bad[:8]}")
+        self.state = {k: v.detach().float().cpu() for k, v in sd.items()}
+
+    def set_source_buffers(self, rand_ini: torch.Tensor, sine_waves: torch.Tensor) -> None:
+        """The causal source's fixed buffers, e.g. a reference model's
+        ``m_source.l_sin_gen.rand_ini`` [1, H] and ``.sine_waves`` [1, N, H]."""
+        self.buffers = {"rand_ini": rand_ini, "sine_waves": sine_waves}
+
+    @torch.no_grad()
+    def finalize_weights(self) -> None:
+        """Fold, pack and upload; create the library handle."""
+        if self.state is None:
+            raise RuntimeError("load_reference_state_dict() first")
+        if self._handle is not None:
+            raise RuntimeError("HiFTVocoder weights have already been finalized")
+        if self.device.type != "cuda":
+            raise ValueError("HiFTVocoder runs on a GPU device")
+        d, sd, dev = self.dims, self.state, self.device
+        H = d.nb_harmonics + 1
+        keep: list[torch.Tensor] = []
+
+        def put(t: torch.Tensor) -> int:
+            t = t.contiguous().to(dev)
+            keep.append(t)
+            return t.data_ptr()
+
+        def folded(name: str, dtype=torch.float32) -> torch.Tensor:
+            if name + ".weight" in sd:
+                return sd[name + ".weight"].to(dtype)
+            g, v = sd[name + _G].to(dtype), sd[name + _V].to(dtype)
+            norm = v.flatten(1).norm(dim=1).view(-1, 1, 1)
+            return v * (g / norm)
+
+        def conv(name: str, dtype=torch.float32, cin_pad: int | None = None) -> list[int]:
+            w = folded(name, dtype)
+            cout, cin, k = w.shape
+            packed = torch.zeros(_ceil(cout, 64), k, cin_pad or _ceil(cin, 16), dtype=dtype)
+            packed[:cout, :, :cin] = w.permute(0, 2, 1)
+            return [put(packed), put(sd[name + ".bias"].to(dtype))]
+
+        def snake(name: str) -> list[int]:
+            a = sd[name + ".alpha"].float()
+            return [put(a), put(1.0 / (a + 1e-9))]
+
+        def resblock(name: str, n_dil: int) -> list[int]:
+            out = []
+            for j in range(n_dil):
+                out += conv(f"{name}.convs1.{j}") + conv(f"{name}.convs2.{j}")
+                out += snake(f"{name}.activations1.{j}") + snake(f"{name}.activations2.{j}")
+            return out
+
+        S = len(d.upsample_rates)
+        K = len(d.resblock_kernel_sizes)
+        D = len(d.resblock_dilation_sizes[0])
+        ptrs = [put(sd["m_source.l_linear.weight"].reshape(H)), put(sd["m_source.l_linear.bias"])]
+        ptrs += conv("conv_pre")
+        for i in range(S):
+            ptrs += conv(f"ups.{i}")
+        for i in range(S):
+            ptrs += conv(f"source_downs.{i}", cin_pad=32)
+        for i in range(S):
+            ptrs += resblock(f"source_resblocks.{i}", D)
+        for i in range(S * K):
+            ptrs += resblock(f"resblocks.{i}", D)
+        ptrs += conv("conv_post")
+        for i in (0, 2, 4, 6, 8):
+            ptrs += conv(f"f0_predictor.condnet.{i}", torch.float64)
+        ptrs += [put(sd["f0_predictor.classifier.weight"].double().reshape(-1)),
+                 put(sd["f0_predictor.classifier.bias"].double())]
+        window = torch.from_numpy(get_window("hann", d.n_fft, fftbins=True).astype(np.float32))
+        buf = self.buffers or random_hift_buffers(d)
+        table = buf["sine_waves"].reshape(-1, H).float()
+        ptrs += [put(window), put(buf["rand_ini"].reshape(H).float()), put(table)]
+        self._cdims.noise_samples = table.shape[0]
+        n = int(self._lib.fcv_hift_weight_count(self._cdims))
+        if n != len(ptrs):
+            raise RuntimeError(f"weight table has {len(ptrs)} entries, the library expects {n}")
+        arr = (_lib.c_void_p * n)(*ptrs)
+        handle = _lib.c_void_p()
+        _lib.check(self._lib.fcv_hift_create(self._cdims, arr, n, handle))
+        self._handle = handle.value
+        self._keep = keep
+        self._ptrs = arr
+
+    def __del__(self):
+        try:
+            if getattr(self, "_handle", None) is not None:
+                self._lib.fcv_hift_destroy(self._handle)
+        except Exception:  # interpreter shutdown: the library may already be unloaded
+            pass
+
+    def _require(self) -> int:
+        if self._handle is None:
+            raise RuntimeError("call finalize_weights() before inference")
+        return self._handle
+
+    # ---- inference -------------------------------------------------------------------------
+
+    def output_samples(self, frames: int, finalize: bool = True) -> int:
+        n = int(self._lib.fcv_hift_output_samples(self._require(), int(frames), int(finalize)))
+        if n < 0:
+            raise ValueError(f"{frames} Mel frames are too few for a "
+                             f"{'final' if finalize else 'non-final'} chunk")
+        return n
+
+    @torch.no_grad()
+    def inference_batched(self, mels: Sequence[torch.Tensor],
+                          finalize_list: Sequence[bool] | None = None,
+                          return_source: bool = False):
+        """Vocode requests of different lengths in one packed pass.  ``mels``: each
+        ``[80, T]`` or ``[1, 80, T]``.  Returns one ``[1, N]`` fp32 waveform per request (and
+        the ``[1, 1, L]`` sources with ``return_source``).  Each waveform equals what
+        ``inference`` gives for that request alone."""
+        h = self._require()
+        mels = [m.reshape(m.shape[-2], m.shape[-1]) for m in mels]
+        if not mels:
+            raise ValueError("no Mel input")
+        fin = [True] * len(mels) if finalize_list is None else [bool(f) for f in finalize_list]
+        if len(fin) != len(mels):
+            raise ValueError("one finalize flag per request is required")
+        speech_all, source_all = [], []
+        for g0 in range(0, len(mels), _lib.HIFT_MAX_DOCS):
+            group = mels[g0:g0 + _lib.HIFT_MAX_DOCS]
+            gfin = fin[g0:g0 + _lib.HIFT_MAX_DOCS]
+            frames = [int(m.shape[1]) for m in group]
+            samples = [self.output_samples(t, f) for t, f in zip(frames, gfin)]
+            f0_frames = [t if f else t - 3 for t, f in zip(frames, gfin)]
+            src_len = [t * self.dims.upsample_scale for t in f0_frames]
+            x = torch.cat([m.to(self.device, torch.float32).transpose(0, 1) for m in group])
+            x = x.contiguous()
+            fr = (_lib.c_int32 * len(group))(*frames)
+            fl = (_lib.c_int32 * len(group))(*[int(f) for f in gfin])
+            need = int(self._lib.fcv_hift_workspace_bytes(h, fr, fl, len(group)))
+            if need == 0:
+                raise ValueError("bad HiFT call layout")
+            if self._ws is None or self._ws.numel() < need:
+                self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+            speech = torch.empty(max(sum(samples), 1), dtype=torch.float32, device=self.device)
+            source = (torch.empty(max(sum(src_len), 1), dtype=torch.float32, device=self.device)
+                      if return_source else None)
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            _lib.check(self._lib.fcv_hift_inference(
+                h, x.data_ptr(), fr, fl, len(group), speech.data_ptr(),
+                source.data_ptr() if source is not None else None, self._ws.data_ptr(),
+                self._ws.numel(), stream))
+            off = 0
+            for n in samples:
+                speech_all.append(speech[off:off + n].view(1, n))
+                off += n
+            if source is not None:
+                off = 0
+                for n in src_len:
+                    source_all.append(source[off:off + n].view(1, 1, n))
+                    off += n
+        return (speech_all, source_all) if return_source else speech_all
+
+    @torch.no_grad()
+    def inference(self, speech_feat: torch.Tensor, finalize: bool = True):
+        """``CausalHiFTGenerator.inference(speech_feat, finalize)`` (generator.py:719-735):
+        ``speech_feat`` ``[B, 80, T]`` -> (waveform ``[B, N]``, source ``[B, 1, L]``)."""
+        if speech_feat.dim() != 3:
+            raise ValueError("speech_feat must be [B, 80, T]")
+        speech, source = self.inference_batched(list(speech_feat), [finalize] * speech_feat.shape[0],
+                                                return_source=True)
+        return torch.cat(speech), torch.cat(source)

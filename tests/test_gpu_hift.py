@@ -1,0 +1,71 @@
+"""GPU parity of the HiFT vocoder (include/fcv_hift.h) against the oracle, whose wiring is pinned
+to the reference generator's own outputs.
+
+Tolerances: the vocoder computes in fp32 (F0 predictor in fp64), so the waveform is within
+rel-L2 1e-4 of the fp32 oracle and the harmonic source within 1e-5 absolute; a request's
+waveform is bit-identical alone and packed with others.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import hift_oracle as H
+from tests.gpu_helpers import rel_l2, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+@pytest.fixture(scope="module")
+def hift(fcv):
+    """The CosyVoice3 HiFT shape with seeded weights and a seeded 64-frame noise table."""
+    dims = fcv.synthetic.HiFTDims()
+    sd = fcv.synthetic.random_hift_state_dict(dims, seed=71)
+    buf = fcv.synthetic.random_hift_buffers(dims, max_samples=480 * 64, seed=72)
+    v = fcv.HiFTVocoder(dims, device="cuda:0", buffers=buf)
+    v.load_reference_state_dict(sd)
+    v.finalize_weights()
+    return dims, H.fold_weight_norm(sd), buf, v
+
+
+@pytest.mark.parametrize("finalize", [True, False])
+def test_vocoder_matches_oracle(hift, finalize):
+    dims, sd, buf, v = hift
+    mel = torch.randn(1, 80, 40, generator=torch.Generator().manual_seed(73))
+    say(f"[hift] 40 frames, finalize={finalize}")
+    speech, s = v.inference(mel.cuda(), finalize=finalize)
+    ref, ref_s = H.inference(sd, mel, buf, dims, finalize)
+    assert speech.shape == ref.shape and s.shape == ref_s.shape
+    es = float((s.cpu() - ref_s).abs().max())
+    ew = rel_l2(speech.cpu(), ref)
+    say(f"[hift] source max abs {es:.2e}, waveform rel_l2 {ew:.2e}")
+    assert es <= 1e-5
+    assert ew <= 1e-4
+
+
+def test_packed_requests_equal_requests_alone(hift):
+    """Three requests of different lengths, final and not: one packed call or one call each
+    gives bit-identical waveforms."""
+    _, _, _, v = hift
+    g = torch.Generator().manual_seed(74)
+    mels = [torch.randn(80, n, generator=g).cuda() for n in (9, 33, 21)]
+    fin = [False, True, True]
+    say("[hift] packed 3 requests")
+    packed = v.inference_batched(mels, fin)
+    for m, f, p in zip(mels, fin, packed):
+        alone = v.inference_batched([m], [f])[0]
+        assert p.shape == alone.shape == (1, v.output_samples(m.shape[1], f))
+        assert torch.equal(p, alone)
+
+
+def test_short_non_final_chunk_is_rejected(hift):
+    _, _, _, v = hift
+    with pytest.raises(ValueError):
+        v.inference_batched([torch.zeros(80, 7, device="cuda")], [False])
