@@ -183,6 +183,69 @@ def frontend_leg(fcv, batch, dev, cpu: bool) -> dict:
     return res
 
 
+HIFT_REPEAT = 3
+
+
+def hift_leg(fcv, batch, dev, cpu: bool) -> dict:
+    """The HiFT vocoder on the generated Mel of the workload's requests (request length minus
+    its prompt), all requests in one packed call: HIP events on the launch stream around
+    HIFT_REPEAT calls; plus the fp32/fp64 oracle on the host for a bounded sample."""
+    import torch
+    dims = fcv.synthetic.HiFTDims()
+    gen = [n - p for n, p in zip(batch.lengths, batch.prompt_lengths)]
+    sd = fcv.synthetic.random_hift_state_dict(dims, seed=0)
+    buf = fcv.synthetic.random_hift_buffers(dims, max_samples=dims.upsample_scale * max(gen),
+                                            seed=1)
+    voc = fcv.HiFTVocoder(dims, device=dev, buffers=buf)
+    voc.load_reference_state_dict(sd)
+    voc.finalize_weights()
+    g = torch.Generator().manual_seed(6)
+    mels = [torch.randn(80, n, generator=g).to(dev) for n in gen]
+    voc.inference_batched(mels)
+    stream = torch.cuda.current_stream(dev)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(HIFT_REPEAT):
+        voc.inference_batched(mels)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / HIFT_REPEAT
+    frames = sum(gen)
+    audio_s = frames * dims.upsample_scale / dims.sampling_rate
+    macs = fcv.synthetic.hift_macs_per_frame(dims)
+    flop = 2.0 * frames * sum(v for k, v in macs.items() if k != "f0_fp64")
+    tflops = flop / (ms * 1e-3) / 1e12
+    res = {
+        "what": "HiFT vocoder, Mel -> 24 kHz waveform, all requests in one packed call (fp32, "
+                "F0 predictor fp64)",
+        "requests": len(gen), "mel_frames": frames, "audio_seconds": round(audio_s, 2),
+        "ms_per_call": round(ms, 3),
+        "audio_seconds_per_second": round(audio_s / (ms * 1e-3), 1),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4),
+                     "flop_per_frame": 2 * sum(v for k, v in macs.items() if k != "f0_fp64"),
+                     "timing": f"HIP events around {HIFT_REPEAT} back-to-back calls; achieved "
+                               "counts the fp32 convolutions of the whole call"},
+    }
+    if cpu:
+        from oracle import hift_oracle as HO
+        threads = len(os.sched_getaffinity(0))
+        torch.set_num_threads(threads)
+        folded = HO.fold_weight_norm(sd)
+        n = min(gen[0], 200)
+        mel = mels[0][:, :n].cpu()[None]
+        t0 = time.perf_counter()
+        HO.inference(folded, mel, buf, dims, True)
+        cpu_s = time.perf_counter() - t0
+        res["cpu_baseline"] = {
+            "value": round(n * dims.upsample_scale / dims.sampling_rate / cpu_s, 2),
+            "unit": "audio seconds per second", "cores": threads, "kind": "port",
+            "sample": f"the first request's first {n} Mel frames through the oracle vocoder "
+                      "(torch CPU conv1d, fp32; F0 in fp64)"}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -192,6 +255,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
     ap.add_argument("--no-frontend", action="store_true", help="skip the flow front-end leg")
+    ap.add_argument("--no-hift", action="store_true", help="skip the HiFT vocoder leg")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one (no hipGraph)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration)")
@@ -300,6 +364,11 @@ def main() -> int:
         log("[bench] flow front-end (tokens -> packed mu rows)")
         frontend = frontend_leg(fcv, batch, dev, cpu=not args.no_cpu_baseline)
 
+    hift = None
+    if not args.no_hift:
+        log("[bench] HiFT vocoder (generated Mel -> waveform)")
+        hift = hift_leg(fcv, batch, dev, cpu=not args.no_cpu_baseline)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (fp32 oracle, padded SDPA)")
@@ -352,6 +421,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "stage_ms": breakdown,
         "frontend": frontend,
+        "hift": hift,
         "eager_ms_per_step": round(eager_wall * 1e3 / K, 4),
     }
     print(json.dumps(out), flush=True)

@@ -282,6 +282,27 @@ def random_hift_state_dict(dims: HiFTDims = HiFTDims(), seed: int = 0,
     return sd
 
 
+def hift_macs_per_frame(d: HiFTDims = HiFTDims()) -> dict[str, int]:
+    """Algorithmic multiply-adds of ``CausalHiFTGenerator.inference`` per Mel frame (real
+    channel counts, no padding): fp32 convolutions by stage, and the fp64 F0 predictor."""
+    spec = d.n_fft + 2
+    out = {"conv_pre": d.in_channels * d.base_channels * (d.conv_pre_look_right + 1)}
+    rows = 1
+    cin = d.base_channels
+    for i, (r, k) in enumerate(zip(d.upsample_rates, d.upsample_kernel_sizes)):
+        rows *= r
+        C = d.stage_channels(i)
+        kd, _ = d.source_down(i)
+        res = sum(len(dil) * 2 * C * C * kk for kk, dil in zip(d.resblock_kernel_sizes,
+                                                               d.resblock_dilation_sizes))
+        src = len(d.source_resblock_dilation_sizes[i]) * 2 * C * C * d.source_resblock_kernel_sizes[i]
+        out[f"stage{i}"] = rows * (cin * C * k + spec * C * kd + res + src)
+        cin = C
+    out["conv_post"] = rows * cin * spec * 7
+    out["f0_fp64"] = d.in_channels * d.f0_channels * 4 + 4 * d.f0_channels * d.f0_channels * 3
+    return out
+
+
 def random_hift_buffers(dims: HiFTDims = HiFTDims(), max_samples: int = 300 * 24000,
                         seed: int = 0) -> dict[str, torch.Tensor]:
     """The causal source's fixed random buffers (generator.py:223-226): initial harmonic
