@@ -5,7 +5,7 @@
 // matrix cores (v_mfma_{f32,f64}_16x16x4): weights are the A operand (rows = output channels),
 // the gathered input rows the B operand, so a lane's four accumulators are four channels of one
 // time step (consecutive in fp32; four apart in fp64, whose 16x16 result is laid out by rows
-// 4 e + lane / 16).  Operands go through LDS K-contiguous, 16 input channels of one tap
+// 4 e + lane / 16).  Operands go through LDS K-contiguous, 32 (or 16) input channels of one tap
 // per chunk, with a register-prefetched double buffer.  A workgroup owns 64 time rows x 64
 // output channels.  Activations that sit between two convolutions are fused: LeakyReLU into the
 // input prologue, bias, ELU, residual add, Snake and the resblock mean into the epilogue, and
@@ -17,8 +17,6 @@
 namespace fcv {
 namespace {
 
-constexpr int kBK = 16;     // input channels per chunk
-constexpr int kPitch = 20;  // LDS row pitch in elements
 constexpr int kTileR = 64;  // time rows per workgroup
 constexpr int kTileC = 64;  // output channels per workgroup
 
@@ -83,11 +81,15 @@ __device__ void conv_store(const HiftConv& p, long row, int cb, int lg,
   }
 }
 
-template <typename T>
+// BK input channels of one tap per chunk (cin_pad % BK == 0); each loader thread moves BK / 16
+// groups of 4 elements per operand, each lane feeds k = 16 m + 4 lg + s at MFMA step (m, s)
+template <typename T, int BK>
 __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const HiftDocs docs) {
   using VT = typename Vec4<T>::type;
-  __shared__ __attribute__((aligned(16))) T sA[2][kTileC][kPitch];
-  __shared__ __attribute__((aligned(16))) T sB[2][kTileR][kPitch];
+  constexpr int PITCH = BK + 4;  // LDS row pitch in elements (conflict-free 16-byte reads)
+  constexpr int G = BK / 16;
+  __shared__ __attribute__((aligned(16))) T sA[2][kTileC][PITCH];
+  __shared__ __attribute__((aligned(16))) T sB[2][kTileR][PITCH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const 
   const int li = lane & 15, lg = lane >> 4;
   const int r0 = blockIdx.x * kTileR;
   const int co0 = blockIdx.y * kTileC;
-  const int cpt = p.cin_pad / kBK;
+  const int cpt = p.cin_pad / BK;
   const int KC = p.k * cpt;
   const long kcin = (long)p.k * p.cin_pad;
 
@@ -114,27 +116,35 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const 
   const T* X = static_cast<const T*>(p.x);
   const T* W = static_cast<const T*>(p.w) + (long)(co0 + lr) * kcin + 4 * lq;
 
-  VT ra, rb;
+  VT ra[G], rb[G];
   auto fetch = [&](int kc) {
     const int tap = kc / cpt;
-    const int c0 = (kc - tap * cpt) * kBK + 4 * lq;
-    ra = *reinterpret_cast<const VT*>(W + (long)kc * kBK);
-    rb = VT{T(0), T(0), T(0), T(0)};
+    const int c0 = (kc - tap * cpt) * BK + 4 * lq;
     const int u = pos * p.stride + tap * p.dil - p.pad;
     const int q = p.up > 1 ? (u >= 0 ? u / p.up : -1) : u;
-    if (valid && q >= 0 && q < in_len) {
-      rb = *reinterpret_cast<const VT*>(X + (long)(in_base + q) * p.ldx + c0);
-      if constexpr (sizeof(T) == 4) {
-        if (p.pro == HIFT_PRO_LEAKY) {
+    const bool live = valid && q >= 0 && q < in_len;
+    const T* xr = X + (long)(in_base + q) * p.ldx + c0;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) rb[e] = rb[e] > 0.0f ? rb[e] : rb[e] * p.slope;
+    for (int m = 0; m < G; ++m) {
+      ra[m] = *reinterpret_cast<const VT*>(W + (long)kc * BK + 16 * m);
+      rb[m] = VT{T(0), T(0), T(0), T(0)};
+      if (live) {
+        rb[m] = *reinterpret_cast<const VT*>(xr + 16 * m);
+        if constexpr (sizeof(T) == 4) {
+          if (p.pro == HIFT_PRO_LEAKY) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rb[m][e] = rb[m][e] > 0.0f ? rb[m][e] : rb[m][e] * p.slope;
+          }
         }
       }
     }
   };
   auto stash = [&](int buf) {
-    *reinterpret_cast<VT*>(&sA[buf][lr][4 * lq]) = ra;
-    *reinterpret_cast<VT*>(&sB[buf][lr][4 * lq]) = rb;
+#pragma unroll
+    for (int m = 0; m < G; ++m) {
+      *reinterpret_cast<VT*>(&sA[buf][lr][16 * m + 4 * lq]) = ra[m];
+      *reinterpret_cast<VT*>(&sB[buf][lr][16 * m + 4 * lq]) = rb[m];
+    }
   };
 
   VT acc[2][2];
@@ -149,19 +159,22 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const 
   for (int kc = 0; kc < KC; ++kc) {
     const int cur = kc & 1;
     if (kc + 1 < KC) fetch(kc + 1);
-    VT av[2], bv[2];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
-      av[a] = *reinterpret_cast<const VT*>(&sA[cur][wc * 32 + a * 16 + li][4 * lg]);
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-      bv[b] = *reinterpret_cast<const VT*>(&sB[cur][wt * 32 + b * 16 + li][4 * lg]);
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int m = 0; m < G; ++m) {
+      VT av[2], bv[2];
 #pragma unroll
       for (int a = 0; a < 2; ++a)
+        av[a] = *reinterpret_cast<const VT*>(&sA[cur][wc * 32 + a * 16 + li][16 * m + 4 * lg]);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) acc[a][b] = mfma_16x16x4(av[a][s], bv[b][s], acc[a][b]);
+      for (int b = 0; b < 2; ++b)
+        bv[b] = *reinterpret_cast<const VT*>(&sB[cur][wt * 32 + b * 16 + li][16 * m + 4 * lg]);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int b = 0; b < 2; ++b) acc[a][b] = mfma_16x16x4(av[a][s], bv[b][s], acc[a][b]);
+    }
     if (kc + 1 < KC) stash(cur ^ 1);
     __syncthreads();
   }
@@ -367,11 +380,18 @@ __global__ __launch_bounds__(256) void istft_ola_kernel(const float* __restrict_
 
 unsigned blocks_for(long n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
+
+
+
 template <typename T>
 hipError_t launch_conv(const HiftConv& p, const HiftDocs& docs, hipStream_t stream) {
   if (p.rows_out <= 0) return hipSuccess;
+  if (p.cin_pad % 16 != 0) return hipErrorInvalidValue;
   const dim3 grid((p.rows_out + kTileR - 1) / kTileR, (p.cout + kTileC - 1) / kTileC);
-  hipLaunchKernelGGL(hift_conv_kernel<T>, grid, dim3(256), 0, stream, p, docs);
+  if (p.cin_pad % 32 == 0)
+    hipLaunchKernelGGL((hift_conv_kernel<T, 32>), grid, dim3(256), 0, stream, p, docs);
+  else
+    hipLaunchKernelGGL((hift_conv_kernel<T, 16>), grid, dim3(256), 0, stream, p, docs);
   return hipGetLastError();
 }
 
