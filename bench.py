@@ -246,6 +246,51 @@ def hift_leg(fcv, batch, dev, cpu: bool) -> dict:
     return res
 
 
+def token2wav_leg(fcv, est, batch, dev) -> dict:
+    """The whole Token2Wav pass for the workload's requests, tokens to waveform: front-end,
+    the packed 10-step CFG solve on the 22-block estimator, HiFT on the generated Mel in one
+    packed call (flashinfer_flow.py:118-184 then token2wav.py:128-131).  Wall time with a
+    device synchronisation on both sides, two calls after one untimed."""
+    import torch
+    fdims = fcv.synthetic.FlowDims()
+    fe = fcv.FlowFrontEnd(device=dev)
+    fe.load_reference_state_dict(fcv.synthetic.random_flow_state_dict(fdims, seed=0))
+    fe.finalize_weights()
+    fe.decoder = fcv.CFMDecoder(est)
+    hdims = fcv.synthetic.HiFTDims()
+    n_tok = [(n + 1) // 2 for n in batch.lengths]
+    p_tok = [p // 2 for p in batch.prompt_lengths]
+    voc = fcv.HiFTVocoder(hdims, device=dev, buffers=fcv.synthetic.random_hift_buffers(
+        hdims, max_samples=hdims.upsample_scale * 2 * max(n_tok), seed=1))
+    voc.load_reference_state_dict(fcv.synthetic.random_hift_state_dict(hdims, seed=0))
+    voc.finalize_weights()
+    g = torch.Generator().manual_seed(7)
+    tokens = [torch.randint(0, fdims.vocab, (n,), generator=g).tolist() for n in n_tok]
+    prompts = [torch.randn(1, 2 * p, 80, generator=g) for p in p_tok]
+    xvec = torch.randn(len(n_tok), 192, generator=g).to(dev)
+
+    def run():
+        mels = fcv.flow_inference_batched(fe, tokens, prompts, xvec)
+        return voc.inference_batched(mels)
+
+    run()
+    times = []
+    for _ in range(2):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        wavs = run()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    sec = min(times)
+    audio = sum(w.shape[1] for w in wavs) / hdims.sampling_rate
+    return {"what": "tokens -> 24 kHz waveform: front-end, 10-step CFG solve (22 blocks, "
+                    "hipGraph), HiFT, all requests packed",
+            "requests": len(n_tok), "tokens": sum(n_tok), "audio_seconds": round(audio, 2),
+            "ms_per_batch": round(sec * 1e3, 2),
+            "audio_seconds_per_second": round(audio / sec, 1),
+            "timing": "wall clock with torch.cuda.synchronize() on both sides, best of 2"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -256,6 +301,8 @@ def main() -> int:
     ap.add_argument("--no-breakdown", action="store_true")
     ap.add_argument("--no-frontend", action="store_true", help="skip the flow front-end leg")
     ap.add_argument("--no-hift", action="store_true", help="skip the HiFT vocoder leg")
+    ap.add_argument("--no-token2wav", action="store_true",
+                    help="skip the end-to-end tokens -> waveform leg")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one (no hipGraph)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration)")
@@ -369,6 +416,11 @@ def main() -> int:
         log("[bench] HiFT vocoder (generated Mel -> waveform)")
         hift = hift_leg(fcv, batch, dev, cpu=not args.no_cpu_baseline)
 
+    t2w = None
+    if not args.no_token2wav:
+        log("[bench] Token2Wav pass (tokens -> waveform)")
+        t2w = token2wav_leg(fcv, est, batch, dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (fp32 oracle, padded SDPA)")
@@ -422,6 +474,7 @@ def main() -> int:
         "stage_ms": breakdown,
         "frontend": frontend,
         "hift": hift,
+        "token2wav": t2w,
         "eager_ms_per_step": round(eager_wall * 1e3 / K, 4),
     }
     print(json.dumps(out), flush=True)

@@ -8,7 +8,8 @@ Sessions and plans are the reference's own objects, used by duck typing: a sessi
 (streaming/session.py:18-27); a plan has ``prefix_len``, ``token_offset``, ``finalize``
 (streaming/chunker.py:14-17).  Vocoding (HiFT) is not part of this path: pass the vocoder as a
 callable with ``hift.inference``'s signature, or leave it out and receive each chunk's new Mel
-frames instead of PCM.
+frames instead of PCM.  When the vocoder is ``HiFTVocoder.inference``, a packed step vocodes
+all of its sessions in one packed call.
 """
 
 from __future__ import annotations
@@ -68,20 +69,35 @@ class StreamingFlow:
         finalize_list = [bool(p.finalize) for p in plans]
         mels = flow_inference_batched_streaming(self.flow, token_list, prompt_feat_list, emb,
                                                 finalize_list)
+        batched = getattr(self.vocoder, "__self__", None)
+        if batched is not None and hasattr(batched, "inference_batched"):
+            # a packed vocoder: every session's Mel cache in one call (same PCM as one call per
+            # session, the vocoder being batch-invariant)
+            for s, p, m in zip(sessions, plans, mels):
+                self._append_mel(s, p, m)
+            speech = batched.inference_batched([s.mel_cache for s in sessions], finalize_list)
+            return [self._emit(s, sp) for s, sp in zip(sessions, speech)]
         return [self._finish_chunk(s, p, m) for s, p, m in zip(sessions, plans, mels)]
+
+    def _append_mel(self, session: Any, plan: Any, mel_full: torch.Tensor) -> torch.Tensor:
+        new_mel = mel_full[:, :, plan.token_offset * self.token_mel_ratio:]
+        session.mel_cache = (new_mel if session.mel_cache is None
+                             else torch.cat([session.mel_cache, new_mel], dim=2))
+        session.chunk_index += 1
+        return new_mel
+
+    @staticmethod
+    def _emit(session: Any, speech: torch.Tensor) -> torch.Tensor:
+        new = speech[:, session.speech_offset:]
+        session.speech_offset += new.shape[1]
+        return new.cpu()
 
     def _finish_chunk(self, session: Any, plan: Any, mel_full: torch.Tensor) -> torch.Tensor:
         """Append the chunk's new Mel frames to the session cache (token2wav.py:188-200); with a
         vocoder, vocode the cache and return only the new PCM on the CPU, else return the new
         Mel frames ``(1, 80, n)``."""
-        new_mel = mel_full[:, :, plan.token_offset * self.token_mel_ratio:]
-        mel = new_mel if session.mel_cache is None else torch.cat([session.mel_cache, new_mel],
-                                                                  dim=2)
-        session.mel_cache = mel
-        session.chunk_index += 1
+        new_mel = self._append_mel(session, plan, mel_full)
         if self.vocoder is None:
             return new_mel
-        speech = self.vocoder(speech_feat=mel, finalize=plan.finalize)[0]
-        new = speech[:, session.speech_offset:]
-        session.speech_offset += new.shape[1]
-        return new.cpu()
+        speech = self.vocoder(speech_feat=session.mel_cache, finalize=plan.finalize)[0]
+        return self._emit(session, speech)

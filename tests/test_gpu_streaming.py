@@ -108,3 +108,34 @@ def test_stream_chunks_match_oracle(fcv, flow2):
         say(f"[stream] chunk {k} new Mel rel_l2 {err:.2e}")
         assert err <= 2e-2
     assert s.mel_cache.shape == (1, 80, 2 * 80) and s.chunk_index == 3
+
+
+def test_stream_step_vocodes_sessions_in_one_packed_call(fcv, flow2):
+    """With HiFTVocoder.inference as the vocoder, a packed step vocodes every session's Mel
+    cache in one call; the PCM equals vocoding each session on its own (a plain callable), bit
+    for bit, over two consecutive chunks."""
+    _, _, fe = flow2
+    dims = fcv.synthetic.HiFTDims()
+    voc = fcv.HiFTVocoder(dims, device="cuda:0",
+                          buffers=fcv.synthetic.random_hift_buffers(dims, max_samples=480 * 400,
+                                                                    seed=46))
+    voc.load_reference_state_dict(fcv.synthetic.random_hift_state_dict(dims, seed=47))
+    voc.finalize_weights()
+    g = torch.Generator().manual_seed(48)
+    sessions = [_session(g, p, n) for p, n in ((0, 60), (12, 80), (30, 50))]
+    alone = copy.deepcopy(sessions)
+    packed_sf = fcv.StreamingFlow(fe, vocoder=voc.inference)
+    plain_sf = fcv.StreamingFlow(fe, vocoder=lambda speech_feat, finalize:
+                                 voc.inference(speech_feat, finalize))
+    steps = [[SimpleNamespace(prefix_len=21, token_offset=0, finalize=False)] * 3,
+             [SimpleNamespace(prefix_len=51, token_offset=18, finalize=False),
+              SimpleNamespace(prefix_len=80, token_offset=18, finalize=True),
+              SimpleNamespace(prefix_len=50, token_offset=18, finalize=True)]]
+    for k, plans in enumerate(steps):
+        say(f"[stream+hift] step {k}")
+        pcm = packed_sf.stream_step_batched(sessions, plans)
+        for i, (s, p) in enumerate(zip(alone, plans)):
+            ref = plain_sf.stream_step(s, p)
+            assert pcm[i].shape == ref.shape and pcm[i].shape[1] > 0
+            assert torch.equal(pcm[i], ref), f"session {i} step {k}"
+            assert sessions[i].speech_offset == s.speech_offset
