@@ -30,6 +30,7 @@ outputs.  ``--only hift`` writes just that file.
 from __future__ import annotations
 
 import argparse
+import json
 import sys
 import types
 from pathlib import Path
@@ -156,6 +157,7 @@ def hift_golden() -> None:
     gen = model.m_source.l_sin_gen
     np.savez_compressed(
         HERE / "hift_small.npz", mel=mel.numpy(), weight_seed=np.int32(61),
+        config=np.array(json.dumps(HIFT_SMALL)),
         rand_ini=gen.rand_ini.numpy(), sine_waves=gen.sine_waves[:, :L].numpy(), **out)
 
 

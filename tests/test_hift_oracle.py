@@ -11,8 +11,8 @@
 
 from __future__ import annotations
 
+import json
 import math
-import sys
 from pathlib import Path
 
 import numpy as np
@@ -22,14 +22,17 @@ import torch
 from oracle import hift_oracle as H
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-sys.path.insert(0, str(GOLDEN))
-from make_golden import HIFT_SMALL  # noqa: E402
+
+
+def _tuples(v):
+    return tuple(_tuples(x) for x in v) if isinstance(v, list) else v
 
 
 @pytest.fixture(scope="module")
 def small(fcv):
     z = np.load(GOLDEN / "hift_small.npz")
-    dims = fcv.synthetic.HiFTDims(**HIFT_SMALL)
+    config = {k: _tuples(v) for k, v in json.loads(str(z["config"])).items()}
+    dims = fcv.synthetic.HiFTDims(**config)
     sd = H.fold_weight_norm(fcv.synthetic.random_hift_state_dict(dims, seed=int(z["weight_seed"])))
     buf = {"rand_ini": torch.from_numpy(z["rand_ini"]), "sine_waves": torch.from_numpy(z["sine_waves"])}
     return z, dims, sd, buf
