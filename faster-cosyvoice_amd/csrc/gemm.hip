@@ -542,6 +542,7 @@ struct EpiQkvRope {
 
 using Tile256x256 = TileCfg<256, 256, 2, 4>;
 using Tile192x256 = TileCfg<192, 256, 2, 4>;
+using Tile160x256 = TileCfg<160, 256, 1, 4>;
 using Tile128x256 = TileCfg<128, 256, 2, 4>;
 using Tile256x128 = TileCfg<256, 128, 4, 2>;
 using Tile128x128 = TileCfg<128, 128, 2, 2>;
@@ -560,13 +561,15 @@ hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, in
 // Tile choice: estimated time = (tiles per CU, rounded up) x tile area / per-CU rate, with the
 // rates measured for each shape at large M with the production epilogues (128x128 runs two
 // workgroups per CU, which its rate includes; 32x128 is rated low so it only wins when the
-// larger shapes leave most CUs idle, as for the 128-column output projection).  The choice only changes which rows and columns
+// larger shapes leave most CUs idle, as for the 128-column output projection; 160x256 (four
+// waves of 160x64) fills 232 of the 256 CUs for the 1024-column GEMMs of a ~9k-row batch,
+// where 192x256 fills 196).  The choice only changes which rows and columns
 // share a workgroup: every output element still accumulates its K slices in the same order, so
 // results are bitwise identical for every tile shape (batch invariance holds).
 constexpr int kCus = 256;
-constexpr int kTileShape[6][2] = {{256, 256}, {192, 256}, {128, 256}, {256, 128}, {128, 128},
-                                   {32, 128}};
-constexpr float kTileRate[6] = {1.0f, 0.97f, 0.88f, 0.81f, 0.87f, 0.45f};
+constexpr int kTileShape[7][2] = {{256, 256}, {192, 256}, {128, 256}, {256, 128}, {128, 128},
+                                   {32, 128}, {160, 256}};
+constexpr float kTileRate[7] = {1.0f, 0.97f, 0.88f, 0.81f, 0.87f, 0.45f, 0.85f};
 
 int g_force_tile = -1;  // >= 0 forces a shape (tuning)
 
@@ -574,7 +577,7 @@ inline int choose_tile(int M, int N) {
   if (g_force_tile >= 0 && N % kTileShape[g_force_tile][1] == 0) return g_force_tile;
   int best = 4;
   float best_t = 3.0e38f;
-  for (int c = 0; c < 6; ++c) {
+  for (int c = 0; c < 7; ++c) {
     const int bm = kTileShape[c][0], bn = kTileShape[c][1];
     if (N % bn != 0) continue;
     const long tiles = (long)((M + bm - 1) / bm) * (N / bn);
@@ -596,6 +599,7 @@ hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, 
     case 2: return launch_tile<Tile128x256>(A, lda, W, ldw, M, N, K, epi, stream);
     case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream);
     case 5: return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream);
+    case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream);
     default: return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream);
   }
 }
