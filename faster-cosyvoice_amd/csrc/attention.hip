@@ -5,7 +5,7 @@
 // l%32 and 16 keys) can be rounded in registers and fed straight back as the B operand of
 // O^T = V^T P^T: no LDS round trip for P.  Each lane therefore owns a single query column,
 // so the online-softmax rescale is a per-lane scalar; the row max / row sum need one
-// cross-lane exchange (lane l <-> l^32).
+// cross-lane exchange (lane l <-> l^32, a v_permlane32_swap).
 //
 // K/V tiles of 64 keys go through LDS double buffers: K row-major [key][dim] and V already
 // transposed [dim][key] (the QKV epilogue writes V transposed), both padded to 72 columns.
@@ -28,6 +28,23 @@ constexpr int LDP = 72;         // padded LDS row (bf16 elements)
 // v_exp_f32 without the library's denormal range reduction: results below 2^-126 flush to 0,
 // which only drops probabilities that are negligible next to the row maximum's 1.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Combine the two wave halves (lane l and lane l ^ 32) without an LDS round trip:
+// v_permlane32_swap of v with itself leaves {v[l], v[l ^ 32]} in lower-half-first order on
+// every lane, so both halves compute the same fp32 result.
+__device__ __forceinline__ float2 half_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ float half_max(float v) {
+  const float2 p = half_pair(v);
+  return fmaxf(p.x, p.y);
+}
+__device__ __forceinline__ float half_sum(float v) {
+  const float2 p = half_pair(v);
+  return p.x + p.y;
+}
 
 __global__ __launch_bounds__(256, 2) void attention_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ VT,
@@ -158,7 +175,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
         }
       }
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+    tmax = half_max(tmax);
     const float m_new = fmaxf(m_run, tmax * scale_log2);
     if (__ballot(m_new > m_run)) {
       // some query of the wave has a new maximum: rescale its partial sums
@@ -202,7 +219,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
     __syncthreads();
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  const float l_tot = half_sum(l_run);
   const float inv = 1.0f / l_tot;
   if (q_row < doc_end) {
     bf16* dst = O + (long)q_row * heads * HD + head * HD;
