@@ -28,6 +28,9 @@ namespace {
 
 constexpr size_t kAlign = 256;
 constexpr int kMaxSteps = 64;
+// solver steps whose AdaLN modulations one pass over the projection weights computes: the
+// skinny-product kernel's row limit, whose rows are each computed exactly as a single row is
+constexpr int kModGroup = 4;
 constexpr int kRowTile = 128;
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -75,10 +78,11 @@ Layout make_layout(const FcvDitDims& d, long rows, long n_docs) {
   L.lens = take(nd * 4);
   L.cu_ext = take((nd + 1) * 4);
   L.tiles = take(n_tiles * 2 * 4);
-  L.mod = take(nd * mod_width * 4);
-  L.tsin = take(nd * 256 * 2);
-  L.t1 = take(nd * (long)d.dim * 2);
-  L.t2 = take(nd * (long)d.dim * 2);
+  const long nt = std::max<long>(nd, kModGroup);  // time rows: per document, or a step group
+  L.mod = take(nt * mod_width * 4);
+  L.tsin = take(nt * 256 * 2);
+  L.t1 = take(nt * (long)d.dim * 2);
+  L.t2 = take(nt * (long)d.dim * 2);
   L.tbuf = take(kMaxSteps * 4);
   L.total = off;
   return L;
@@ -147,24 +151,55 @@ struct FcvDit {
 
 namespace {
 
-int run_forward_body(FcvDit* m, const float* x, const float* mu, const float* cond,
-                     const float* spks, const float* t, int n_t, float* v_out, hipStream_t s);
+// timestep embedding -> SiLU(temb) -> every block's AdaLN modulation in one projection, for
+// n_t time values: row i of the `mod` region (mod_width floats) belongs to t[i]
+// (TimestepEmbedding modules.py:606-616; _project_modulations flashinfer_dit.py:430-445)
+int compute_modulations(FcvDit* m, const float* t, int n_t, hipStream_t s) {
+  const FcvDitWeights& w = m->w;
+  const int D = m->dims.dim;
+  auto B = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
+  float* mod = m->at<float>(m->L.mod);
+  bf16* tsin = m->at<bf16>(m->L.tsin);
+  bf16* t1 = m->at<bf16>(m->L.t1);
+  bf16* t2 = m->at<bf16>(m->L.t2);
+  FCV_HIP(fcv::timestep_sinusoid(t, n_t, 256, tsin, s));
+  FCV_HIP(fcv::gemm_bias_silu_bf16(tsin, 256, B(w.temb_w1), 256, w.temb_b1, n_t, D, 256, t1, D, s));
+  FCV_HIP(fcv::gemm_bias_silu_bf16(t1, D, B(w.temb_w2), D, w.temb_b2, n_t, D, D, t2, D, s));
+  FCV_HIP(m->probe_begin(FCV_STAGE_ADALN, -1, s));
+  for (int rep = m->launches(FCV_STAGE_ADALN, -1); rep > 0; --rep)
+    FCV_HIP(fcv::gemm_bias_f32(t2, D, B(w.ada_w), D, w.ada_b, n_t, (int)m->mod_width, D, mod,
+                               (int)m->mod_width, (int)m->mod_width, s));
+  FCV_HIP(m->probe_end(FCV_STAGE_ADALN, -1, s));
+  return FCV_OK;
+}
 
+int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
+               const float* mod, long mod_stride, float* v_out, hipStream_t s);
+
+// one estimator evaluation: modulations for t (1 shared value or one per document), then the
+// network; `mod_row`, when not null, is an already computed shared-t modulation row
 int run_forward(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
-                const float* t, int n_t, float* v_out, hipStream_t s) {
+                const float* t, int n_t, const float* mod_row, float* v_out, hipStream_t s) {
   FCV_HIP(m->probe_begin(FCV_STAGE_FORWARD, -1, s));
-  int rc = run_forward_body(m, x, mu, cond, spks, t, n_t, v_out, s);
+  const float* mod = mod_row;
+  long mod_stride = 0;
+  if (!mod) {
+    int rc = compute_modulations(m, t, n_t, s);
+    if (rc != FCV_OK) return rc;
+    mod = m->at<float>(m->L.mod);
+    mod_stride = (n_t == 1) ? 0 : m->mod_width;
+  }
+  int rc = run_blocks(m, x, mu, cond, spks, mod, mod_stride, v_out, s);
   if (rc != FCV_OK) return rc;
   FCV_HIP(m->probe_end(FCV_STAGE_FORWARD, -1, s));
   return FCV_OK;
 }
 
-int run_forward_body(FcvDit* m, const float* x, const float* mu, const float* cond,
-                     const float* spks, const float* t, int n_t, float* v_out, hipStream_t s) {
+int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
+               const float* mod, long mod_stride, float* v_out, hipStream_t s) {
   const FcvDitDims& d = m->dims;
   const FcvDitWeights& w = m->w;
   const int R = m->rows_int, D = d.dim, F = d.ff_dim, mel = d.mel_dim;
-  const long mod_stride = (n_t == 1) ? 0 : m->mod_width;
   auto B = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
 
   float* h = m->at<float>(m->L.h);
@@ -181,21 +216,6 @@ int run_forward_body(FcvDit* m, const float* x, const float* mu, const float* co
   int32_t* cu_int = m->at<int32_t>(m->L.cu_int);
   int32_t* lens = m->at<int32_t>(m->L.lens);
   int32_t* tiles = m->at<int32_t>(m->L.tiles);
-  float* mod = m->at<float>(m->L.mod);
-  bf16* tsin = m->at<bf16>(m->L.tsin);
-  bf16* t1 = m->at<bf16>(m->L.t1);
-  bf16* t2 = m->at<bf16>(m->L.t2);
-
-  // timestep embedding -> SiLU(temb) -> every block's AdaLN modulation in one projection
-  // (TimestepEmbedding modules.py:606-616; _project_modulations flashinfer_dit.py:430-445)
-  FCV_HIP(fcv::timestep_sinusoid(t, n_t, 256, tsin, s));
-  FCV_HIP(fcv::gemm_bias_silu_bf16(tsin, 256, B(w.temb_w1), 256, w.temb_b1, n_t, D, 256, t1, D, s));
-  FCV_HIP(fcv::gemm_bias_silu_bf16(t1, D, B(w.temb_w2), D, w.temb_b2, n_t, D, D, t2, D, s));
-  FCV_HIP(m->probe_begin(FCV_STAGE_ADALN, -1, s));
-  for (int rep = m->launches(FCV_STAGE_ADALN, -1); rep > 0; --rep)
-    FCV_HIP(fcv::gemm_bias_f32(t2, D, B(w.ada_w), D, w.ada_b, n_t, (int)m->mod_width, D, mod,
-                               (int)m->mod_width, (int)m->mod_width, s));
-  FCV_HIP(m->probe_end(FCV_STAGE_ADALN, -1, s));
 
   // input projection + causal conv position embedding (InputEmbedding dit.py:84-98)
   FCV_HIP(fcv::pack_inputs(x, cond, mu, spks, docid, ext_row, R, mel, ain, s));
@@ -419,7 +439,7 @@ int fcv_dit_forward(FcvDit* m, const float* x, const float* mu, const float* con
             "spks and cond are required (null input pointer)");
   FCV_CHECK(n_t == 1 || n_t == m->n_docs, FCV_ERR_INVALID, "n_t must be 1 or n_docs");
   m->probe_count = 0;
-  return run_forward(m, x, mu, cond, spks, t, n_t, v_out, s);
+  return run_forward(m, x, mu, cond, spks, t, n_t, nullptr, v_out, s);
 }
 
 static int check_cfg_layout(const FcvDit* m) {
@@ -458,8 +478,15 @@ int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const
 
   auto body = [&]() -> int {
     m->probe_count = 0;
+    const float* mod = m->at<float>(m->L.mod);
     for (int step = 0; step < n_steps; ++step) {
-      int r = run_forward(m, x, mu, cond, spks, tbuf + step, 1, vbuf, s);
+      // every kModGroup steps, one pass over the AdaLN weights gives the next steps' rows
+      if (step % kModGroup == 0) {
+        int r = compute_modulations(m, tbuf + step, std::min(kModGroup, n_steps - step), s);
+        if (r != FCV_OK) return r;
+      }
+      int r = run_forward(m, x, mu, cond, spks, nullptr, 1, mod + (step % kModGroup) * m->mod_width,
+                          vbuf, s);
       if (r != FCV_OK) return r;
       FCV_HIP(m->probe_begin(FCV_STAGE_EULER, -1, s));
       FCV_HIP(fcv::euler_cfg_update(x, vbuf, rcond, mel, dt_host[step], cfg, s));
