@@ -116,8 +116,11 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const 
   const T* X = static_cast<const T*>(p.x);
   const T* W = static_cast<const T*>(p.w) + (long)(co0 + lr) * kcin + 4 * lq;
 
-  VT ra[G], rb[G];
-  auto fetch = [&](int kc) {
+  // Two register sets: the loads of chunk kc + 2 are issued while chunk kc is computed and
+  // chunk kc + 1 (loaded one iteration earlier) is written to LDS, so every load has about two
+  // chunk computations to arrive.  The sets are picked by compile-time index (loop unrolled by 2).
+  VT ra[2][G], rb[2][G];
+  auto fetch = [&](int kc, VT (&a)[G], VT (&b)[G]) {
     const int tap = kc / cpt;
     const int c0 = (kc - tap * cpt) * BK + 4 * lq;
     const int u = pos * p.stride + tap * p.dil - p.pad;
@@ -126,24 +129,24 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const 
     const T* xr = X + (long)(in_base + q) * p.ldx + c0;
 #pragma unroll
     for (int m = 0; m < G; ++m) {
-      ra[m] = *reinterpret_cast<const VT*>(W + (long)kc * BK + 16 * m);
-      rb[m] = VT{T(0), T(0), T(0), T(0)};
-      if (live) {
-        rb[m] = *reinterpret_cast<const VT*>(xr + 16 * m);
-        if constexpr (sizeof(T) == 4) {
-          if (p.pro == HIFT_PRO_LEAKY) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) rb[m][e] = rb[m][e] > 0.0f ? rb[m][e] : rb[m][e] * p.slope;
-          }
-        }
-      }
+      a[m] = *reinterpret_cast<const VT*>(W + (long)kc * BK + 16 * m);
+      b[m] = VT{T(0), T(0), T(0), T(0)};
+      if (live) b[m] = *reinterpret_cast<const VT*>(xr + 16 * m);
     }
   };
-  auto stash = [&](int buf) {
+  // the input prologue runs here, when the data is needed, so fetch never waits for its loads
+  auto stash = [&](int buf, const VT (&a)[G], const VT (&b)[G]) {
 #pragma unroll
     for (int m = 0; m < G; ++m) {
-      *reinterpret_cast<VT*>(&sA[buf][lr][16 * m + 4 * lq]) = ra[m];
-      *reinterpret_cast<VT*>(&sB[buf][lr][16 * m + 4 * lq]) = rb[m];
+      VT bm = b[m];
+      if constexpr (sizeof(T) == 4) {
+        if (p.pro == HIFT_PRO_LEAKY) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bm[e] = bm[e] > 0.0f ? bm[e] : bm[e] * p.slope;
+        }
+      }
+      *reinterpret_cast<VT*>(&sA[buf][lr][16 * m + 4 * lq]) = a[m];
+      *reinterpret_cast<VT*>(&sB[buf][lr][16 * m + 4 * lq]) = bm;
     }
   };
 
@@ -153,12 +156,7 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const 
 #pragma unroll
     for (int b = 0; b < 2; ++b) acc[a][b] = VT{T(0), T(0), T(0), T(0)};
 
-  fetch(0);
-  stash(0);
-  __syncthreads();
-  for (int kc = 0; kc < KC; ++kc) {
-    const int cur = kc & 1;
-    if (kc + 1 < KC) fetch(kc + 1);
+  auto compute = [&](int cur) {
 #pragma unroll
     for (int m = 0; m < G; ++m) {
       VT av[2], bv[2];
@@ -175,7 +173,23 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const 
 #pragma unroll
           for (int b = 0; b < 2; ++b) acc[a][b] = mfma_16x16x4(av[a][s], bv[b][s], acc[a][b]);
     }
-    if (kc + 1 < KC) stash(cur ^ 1);
+  };
+
+  fetch(0, ra[0], rb[0]);
+  if (KC > 1) fetch(1, ra[1], rb[1]);
+  stash(0, ra[0], rb[0]);
+  __syncthreads();
+  for (int kc = 0; kc < KC; kc += 2) {
+    // chunk kc is in LDS buffer 0; register set 1 holds chunk kc + 1
+    if (kc + 2 < KC) fetch(kc + 2, ra[0], rb[0]);
+    compute(0);
+    if (kc + 1 < KC) stash(1, ra[1], rb[1]);
+    __syncthreads();
+    if (kc + 1 >= KC) break;
+    // chunk kc + 1 is in buffer 1; register set 0 holds chunk kc + 2
+    if (kc + 3 < KC) fetch(kc + 3, ra[1], rb[1]);
+    compute(1);
+    if (kc + 2 < KC) stash(0, ra[0], rb[0]);
     __syncthreads();
   }
 
