@@ -451,6 +451,8 @@ def main() -> int:
             "depth": 22, "dim": 1024, "heads": 16,
             "graph": "none (eager launches)" if args.eager else "hipGraph of the K-step solve",
         },
+        # rows count both CFG halves; a request's frames appear once per half
+        "request_frames_per_s": round(value / 2, 1),
         "mfma_util_pct": round(100 * mfma_util, 2),
         "tflops_per_step": round(flops["total"] / 1e12, 4),
         "roofline": {
