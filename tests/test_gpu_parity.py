@@ -105,6 +105,31 @@ def test_long_document(fcv, stress2, streaming):
     assert e_long <= BF16_W_TOL and e_short <= BF16_W_TOL
 
 
+@pytest.mark.parametrize("streaming", [False, True])
+def test_max_pos_document_among_many_tiny_ones(fcv, stress2, streaming):
+    """Size limits: one document exactly as long as the RoPE tables (max_pos rows, so its last
+    query reads the tables' last row; 4096 as in the reference's finalize_weights,
+    flashinfer_dit.py:262-273) packed with 150 documents of 1..40 frames (150 entries in every
+    per-document table, many one-tile documents, most shorter than one 50-frame chunk)."""
+    sd, _ = stress2
+    est = make_estimator(fcv, sd, depth=2, max_pos=4096)
+    g = torch.Generator().manual_seed(17)
+    tiny = torch.randint(1, 41, (150,), generator=g).tolist()
+    lengths = tiny[:75] + [est.max_pos] + tiny[75:]
+    x, mu, cond, spks, t = random_packed(lengths, seed=19)
+    say(f"[limits] streaming={streaming} {len(lengths)} docs, {sum(lengths)} rows, GPU forward")
+    v = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming).cpu()
+    say(f"[limits] streaming={streaming} oracle forward")
+    ref = oracle_packed(bf16_weights(sd), x, mu, cond, spks, t, lengths, streaming)
+    off, worst = 0, 0.0
+    for n in lengths:
+        e = rel_l2(v[off:off + n], ref[off:off + n])
+        worst = max(worst, e)
+        assert e <= BF16_W_TOL, f"document of {n} rows at row {off}: rel_l2 {e:.2e}"
+        off += n
+    say(f"[limits] streaming={streaming} worst per-document rel_l2 {worst:.2e}")
+
+
 def test_shared_t_equals_per_doc_t(fcv, stress2):
     """One shared t vs the same t per document.  Up to 4 t rows the time MLP and the AdaLN
     projection take the same bandwidth-bound path either way (bitwise equal); with more rows
