@@ -571,10 +571,7 @@ constexpr int kTileShape[7][2] = {{256, 256}, {192, 256}, {128, 256}, {256, 128}
                                    {32, 128}, {160, 256}};
 constexpr float kTileRate[7] = {1.0f, 0.97f, 0.88f, 0.81f, 0.87f, 0.45f, 0.85f};
 
-int g_force_tile = -1;  // >= 0 forces a shape (tuning)
-
 inline int choose_tile(int M, int N) {
-  if (g_force_tile >= 0 && N % kTileShape[g_force_tile][1] == 0) return g_force_tile;
   int best = 4;
   float best_t = 3.0e38f;
   for (int c = 0; c < 7; ++c) {
