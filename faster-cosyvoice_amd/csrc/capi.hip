@@ -111,10 +111,10 @@ struct FcvDit {
   int probe_repeat = 1;
   std::vector<hipEvent_t> probe_events;
 
-  // graph cache
+  // graph cache: the captured solve and its key; seen_key is the previous solve's key
   hipGraphExec_t graph_exec = nullptr;
-  unsigned long graph_generation = 0;
   std::vector<uintptr_t> graph_key;
+  std::vector<uintptr_t> seen_key;
 
   template <class T>
   T* at(size_t off) const { return reinterpret_cast<T*>(ws + off); }
@@ -494,8 +494,7 @@ int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const
     }
     return FCV_OK;
   };
-  if (!use_graph) return body();
-
+  // what a captured loop bakes in: the plan, the buffers and the schedule (t is read from tbuf)
   std::vector<uintptr_t> key = {m->generation, (uintptr_t)x, (uintptr_t)mu, (uintptr_t)cond,
                                 (uintptr_t)spks, (uintptr_t)n_steps};
   uint32_t bits;
@@ -505,7 +504,14 @@ int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const
     std::memcpy(&bits, &dt_host[i], 4);
     key.push_back(bits);
   }
-  if (!m->graph_exec || key != m->graph_key) {
+  const bool cached = m->graph_exec && key == m->graph_key;
+  // Capturing and instantiating the loop costs more than running it once eagerly, so a key is
+  // captured on its second solve: a layout used once (a streaming step) never pays for a capture.
+  if (!use_graph || (!cached && key != m->seen_key)) {
+    m->seen_key = key;
+    return body();
+  }
+  if (!cached) {
     m->drop_graph();
     FCV_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     int r = body();

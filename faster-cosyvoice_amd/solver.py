@@ -1,7 +1,10 @@
 """Packed CFG Euler solver over ``DiTEstimator`` (flashinfer_flow.py:16-74).
 
 ``solve_euler_packed`` keeps the sample packed and fp32 across steps and runs the whole
-n-step loop inside libfcvdit (``fcv_dit_solve``), optionally captured once in a hipGraph.
+n-step loop inside libfcvdit (``fcv_dit_solve``).  With ``use_graph`` the loop is replayed from
+a hipGraph once the same layout and buffers come back: a layout's first solve runs eagerly and
+its second captures the graph, since a capture costs more than one eager run (a streaming
+step, whose layout is new every call, never captures).
 ``solve_euler_batched`` keeps the reference's padded signature for callers that hand it
 ``[B,80,T]`` tensors and a padding mask.
 """

@@ -107,8 +107,11 @@ int fcv_euler_cfg_step(FcvDit* dit, float* x, const float* v, float dt, float cf
  * batch: n_steps x (forward with t_host[step] shared by all documents, then the CFG Euler
  * update with dt_host[step]).  x: [rows][mel], both halves equal on entry, updated in place.
  * mu/cond/spks as in fcv_dit_forward (zeros in the unconditional half).  use_graph != 0
- * captures the whole loop once into a hipGraph (re-captured when the plan, the pointers or
- * the schedule change) and replays it.  n_steps <= 64. */
+ * replays a hipGraph of the whole loop when the plan, the pointers and the schedule (dt_host,
+ * cfg, n_steps) match the cached graph's; a solve with a new key runs eagerly, and the next
+ * solve with that same key captures it (a capture costs more than one eager run, so a layout
+ * used once, as in streaming, is never captured).  Results are identical either way.
+ * n_steps <= 64. */
 int fcv_dit_solve(FcvDit* dit, float* x, const float* mu, const float* cond, const float* spks,
                   const float* t_host, const float* dt_host, int32_t n_steps, float cfg,
                   int32_t use_graph, hipStream_t stream);
