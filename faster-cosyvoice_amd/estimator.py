@@ -79,10 +79,81 @@ class _Block(nn.Module):
         self.ff = _FeedForward(dim, ff_dim, device)
 
 
+# ---- one library handle: workspace, packed-layout plan, launch stream ---------------------------
+
+
+class _PackedRunner:
+    """A libfcvdit handle with its own workspace, plan cache and launch stream.
+
+    The estimator is one; ``_Lane`` objects are more handles over the same derived weights, so
+    that independent groups of documents can run on concurrent streams.  Subclasses set
+    ``device``, ``static_chunk_size`` and ``_handle``."""
+
+    def _init_runner(self) -> None:
+        self._workspace: torch.Tensor | None = None
+        self._plan_key: tuple | None = None
+        self._stream: torch.cuda.Stream | None = None
+        self.plan_calls = 0
+
+    def _require(self) -> int:
+        if self._handle is None:
+            raise RuntimeError("call finalize_weights() before running the estimator")
+        return self._handle
+
+    def plan(self, seqlens: Sequence[int], streaming: bool = False) -> None:
+        """Plan the packed layout (FlashInfer ``plan`` equivalent); no-op when unchanged."""
+        handle = self._require()
+        lengths = tuple(int(n) for n in seqlens)
+        key = (lengths, bool(streaming))
+        if key == self._plan_key:
+            return
+        lib = _lib.load()
+        rows = sum(lengths)
+        need = lib.fcv_dit_workspace_bytes(handle, rows, len(lengths))
+        if self._workspace is None or self._workspace.numel() < need:
+            cap = max(need, 2 * (0 if self._workspace is None else self._workspace.numel()))
+            self._workspace = None
+            self._workspace = torch.empty(cap + 256, dtype=torch.uint8, device=self.device)
+        base = self._workspace.data_ptr()
+        aligned = (base + 255) // 256 * 256
+        cu = [0]
+        for n in lengths:
+            cu.append(cu[-1] + n)
+        cu_arr = (_lib.c_int32 * len(cu))(*cu)
+        mode = _lib.FCV_MASK_CHUNK_CAUSAL if streaming else _lib.FCV_MASK_FULL
+        _lib.check(lib.fcv_dit_plan(handle, cu_arr, len(lengths), mode, self.static_chunk_size,
+                                    aligned, self._workspace.numel() - (aligned - base),
+                                    self._stream_ptr()))
+        self._plan_key = key
+        self.plan_calls += 1
+
+    def _stream_ptr(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+
+class _Lane(_PackedRunner):
+    """A second handle over an estimator's derived weights (which the estimator keeps alive)."""
+
+    def __init__(self, owner: "DiTEstimator", handle: int):
+        self.device = owner.device
+        self.static_chunk_size = owner.static_chunk_size
+        self.dims = owner.dims
+        self._handle = handle
+        self._owner = owner
+        self._init_runner()
+
+    def __del__(self):
+        handle = getattr(self, "_handle", None)
+        lib = getattr(_lib, "_LIB", None) if _lib is not None else None
+        if handle is not None and lib is not None:
+            lib.fcv_dit_destroy(handle)
+            self._handle = None
+
+
 # ---- the estimator ----------------------------------------------------------------------------
 
 
-class DiTEstimator(nn.Module):
+class DiTEstimator(nn.Module, _PackedRunner):
     """Packed-batch CosyVoice3 DiT estimator on gfx950 HIP kernels.
 
     Mirrors ``FlashInferDiT`` (flashinfer_dit.py:98-186): construct, ``load_state_dict``,
@@ -124,10 +195,9 @@ class DiTEstimator(nn.Module):
 
         self._handle: int | None = None
         self._derived: dict[str, torch.Tensor] = {}
-        self._workspace: torch.Tensor | None = None
-        self._plan_key: tuple | None = None
-        self._stream: torch.cuda.Stream | None = None
-        self.plan_calls = 0
+        self._create_args: tuple | None = None
+        self._extra_lanes: list[_Lane] = []
+        self._init_runner()
 
     # -- loading ----------------------------------------------------------------------------
 
@@ -239,6 +309,7 @@ class DiTEstimator(nn.Module):
         _lib.check(lib.fcv_dit_create(dims, weights, handle))
         self._handle = handle.value
         self._derived = out
+        self._create_args = (dims, weights)
         # the derived copies are the only ones the kernels read; free the parameter storage
         for p in self.parameters():
             p.data = torch.empty(0)
@@ -250,42 +321,18 @@ class DiTEstimator(nn.Module):
             lib.fcv_dit_destroy(handle)
             self._handle = None
 
-    # -- planning ---------------------------------------------------------------------------
+    # -- concurrent lanes -------------------------------------------------------------------
 
-    def _require(self) -> int:
-        if self._handle is None:
-            raise RuntimeError("call finalize_weights() before running the estimator")
-        return self._handle
-
-    def plan(self, seqlens: Sequence[int], streaming: bool = False) -> None:
-        """Plan the packed layout (FlashInfer ``plan`` equivalent); no-op when unchanged."""
-        handle = self._require()
-        lengths = tuple(int(n) for n in seqlens)
-        key = (lengths, bool(streaming))
-        if key == self._plan_key:
-            return
+    def lanes(self, n: int) -> list[_PackedRunner]:
+        """``n`` runners over this estimator's weights: the estimator itself, then extra
+        handles created on first use (each with its own workspace, plan and stream)."""
         lib = _lib.load()
-        rows = sum(lengths)
-        need = lib.fcv_dit_workspace_bytes(handle, rows, len(lengths))
-        if self._workspace is None or self._workspace.numel() < need:
-            cap = max(need, 2 * (0 if self._workspace is None else self._workspace.numel()))
-            self._workspace = None
-            self._workspace = torch.empty(cap + 256, dtype=torch.uint8, device=self.device)
-        base = self._workspace.data_ptr()
-        aligned = (base + 255) // 256 * 256
-        cu = [0]
-        for n in lengths:
-            cu.append(cu[-1] + n)
-        cu_arr = (_lib.c_int32 * len(cu))(*cu)
-        mode = _lib.FCV_MASK_CHUNK_CAUSAL if streaming else _lib.FCV_MASK_FULL
-        _lib.check(lib.fcv_dit_plan(handle, cu_arr, len(lengths), mode, self.static_chunk_size,
-                                    aligned, self._workspace.numel() - (aligned - base),
-                                    self._stream_ptr()))
-        self._plan_key = key
-        self.plan_calls += 1
-
-    def _stream_ptr(self) -> int:
-        return torch.cuda.current_stream(self.device).cuda_stream
+        self._require()
+        while len(self._extra_lanes) < n - 1:
+            handle = _lib.c_void_p()
+            _lib.check(lib.fcv_dit_create(*self._create_args, handle))
+            self._extra_lanes.append(_Lane(self, handle.value))
+        return [self] + self._extra_lanes[: n - 1]
 
     # -- compute ----------------------------------------------------------------------------
 

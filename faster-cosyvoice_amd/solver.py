@@ -17,7 +17,7 @@ from typing import Any
 import torch
 
 from . import _lib
-from .estimator import DiTEstimator
+from .estimator import DiTEstimator, _PackedRunner
 
 
 def euler_schedule(n_steps: int) -> tuple[list[float], list[float]]:
@@ -38,36 +38,77 @@ def euler_schedule(n_steps: int) -> tuple[list[float], list[float]]:
     return ts, dts
 
 
-def _solver_buffers(estimator: DiTEstimator, rc: int, n_req: int) -> dict[str, torch.Tensor]:
+def _solver_buffers(runner: _PackedRunner, dims, rc: int, n_req: int) -> dict[str, torch.Tensor]:
     """Packed CFG input buffers [2*rc, 80] (zero second halves) reused while the shape holds."""
     key = (rc, n_req)
-    bufs = getattr(estimator, "_solver_bufs", None)
+    bufs = getattr(runner, "_solver_bufs", None)
     if bufs is None or bufs["key"] != key:
-        mel, dev = estimator.dims.mel_dim, estimator.device
+        mel, dev = dims.mel_dim, runner.device
         z = lambda rows: torch.zeros(rows, mel, dtype=torch.float32, device=dev)
         bufs = {"key": key, "x": z(2 * rc), "mu": z(2 * rc), "cond": z(2 * rc), "spks": z(2 * n_req)}
-        estimator._solver_bufs = bufs
+        runner._solver_bufs = bufs
     return bufs
 
 
-def _stream_for(estimator: DiTEstimator) -> torch.cuda.Stream:
+def _stream_for(runner: _PackedRunner) -> torch.cuda.Stream:
     # hipGraph capture needs a non-default stream; default priority as required.
-    if estimator._stream is None:
-        estimator._stream = torch.cuda.Stream(device=estimator.device)
-    return estimator._stream
+    if runner._stream is None:
+        runner._stream = torch.cuda.Stream(device=runner.device)
+    return runner._stream
 
 
-@torch.no_grad()
+def request_groups(lengths: Sequence[int], n_groups: int) -> list[list[int]]:
+    """Requests split into ``n_groups`` groups of about equal DiT cost, per request
+    ``378 MFLOP x L + 90 kFLOP x L^2`` (dense rows, attention pairs), longest first onto the
+    least loaded group.  Empty groups are dropped; each group lists its requests in order."""
+    cost = lambda n: n * n + 4200 * n
+    groups: list[list[int]] = [[] for _ in range(max(1, n_groups))]
+    load = [0] * len(groups)
+    for i in sorted(range(len(lengths)), key=lambda i: -cost(lengths[i])):
+        g = load.index(min(load))
+        groups[g].append(i)
+        load[g] += cost(lengths[i])
+    return [sorted(g) for g in groups if g]
+
+
+def _solve_on(runner: _PackedRunner, dims, noise: torch.Tensor, mu: torch.Tensor,
+              cond: torch.Tensor, spks: torch.Tensor, lengths: list[int], t_arr, dt_arr,
+              n_steps: int, cfg_rate: float, streaming: bool, use_graph: bool,
+              stream: torch.cuda.Stream) -> torch.Tensor:
+    """One packed CFG solve on ``runner``, enqueued on ``stream`` (the caller orders it)."""
+    rc = sum(lengths)
+    with torch.cuda.stream(stream):
+        runner.plan(lengths + lengths, streaming)
+        # persistent solver buffers: stable pointers let a captured graph be replayed
+        buf = _solver_buffers(runner, dims, rc, len(lengths))
+        buf["x"][:rc].copy_(noise)
+        buf["x"][rc:].copy_(noise)
+        buf["mu"][:rc].copy_(mu)
+        buf["cond"][:rc].copy_(cond)
+        buf["spks"][: len(lengths)].copy_(spks)
+        _lib.check(_lib.load().fcv_dit_solve(
+            runner._require(), buf["x"].data_ptr(), buf["mu"].data_ptr(),
+            buf["cond"].data_ptr(), buf["spks"].data_ptr(), t_arr, dt_arr, n_steps,
+            float(cfg_rate), int(bool(use_graph)), stream.cuda_stream))
+        return buf["x"][:rc].clone()
+
+
 def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.Tensor,
                        cond: torch.Tensor, spks: torch.Tensor, lengths: Sequence[int],
                        n_steps: int = 10, cfg_rate: float = 0.7, streaming: bool = False,
-                       use_graph: bool = True) -> torch.Tensor:
+                       use_graph: bool = True, concurrency: int | None = None) -> torch.Tensor:
     """CFG Euler solve on packed request rows.
 
     noise, mu, cond: ``[Rc, 80]`` conditional rows of the B requests (doc-major);
-    spks: ``[B, 80]``; lengths: the B request lengths.  The 2B-document CFG batch
-    ``[cond..., uncond...]`` (zero mu/cond/spks in the second half) is planned once and
-    the result ``[Rc, 80]`` fp32 is the sample after ``n_steps`` steps.
+    spks: ``[B, 80]``; lengths: the B request lengths.  The result ``[Rc, 80]`` fp32 is the
+    sample after ``n_steps`` steps.
+
+    The requests run as ``concurrency`` groups (default: 2 when there are at least 2
+    requests), each a packed CFG batch ``[cond..., uncond...]`` (zero mu/cond/spks in the
+    second half) on its own handle over the shared weights and its own stream, all launched
+    before any is waited for.  One group's tail rounds and bandwidth-bound phases then overlap
+    the other's matrix work.  A document's result does not depend on what it is packed with,
+    so the rows are bit-identical to one packed batch of all requests.
     """
     lengths = [int(n) for n in lengths]
     rc = sum(lengths)
@@ -78,26 +119,45 @@ def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.T
         raise ValueError(f"noise, mu and cond must hold {rc} rows")
     if spks.shape[0] != len(lengths):
         raise ValueError("spks must hold one row per request")
+    n_groups = (2 if len(lengths) >= 2 else 1) if concurrency is None else int(concurrency)
+    if n_groups < 1:
+        raise ValueError("concurrency must be >= 1")
+    groups = request_groups(lengths, n_groups)
     ts, dts = euler_schedule(n_steps)
-    stream = _stream_for(estimator)
-    stream.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(stream):
-        estimator.plan(lengths + lengths, streaming)
-        # persistent solver buffers: stable pointers let a captured graph be replayed
-        buf = _solver_buffers(estimator, rc, len(lengths))
-        buf["x"][:rc].copy_(noise)
-        buf["x"][rc:].copy_(noise)
-        buf["mu"][:rc].copy_(mu)
-        buf["cond"][:rc].copy_(cond)
-        buf["spks"][: len(lengths)].copy_(spks)
-        t_arr = (_lib.c_float * n_steps)(*ts)
-        dt_arr = (_lib.c_float * n_steps)(*dts)
-        _lib.check(_lib.load().fcv_dit_solve(
-            estimator._require(), buf["x"].data_ptr(), buf["mu"].data_ptr(),
-            buf["cond"].data_ptr(), buf["spks"].data_ptr(), t_arr, dt_arr, n_steps,
-            float(cfg_rate), int(bool(use_graph)), stream.cuda_stream))
-        result = buf["x"][:rc].clone()
-    torch.cuda.current_stream(dev).wait_stream(stream)
+    t_arr = (_lib.c_float * n_steps)(*ts)
+    dt_arr = (_lib.c_float * n_steps)(*dts)
+    current = torch.cuda.current_stream(dev)
+    runners = estimator.lanes(len(groups))
+    if len(groups) == 1:
+        stream = _stream_for(estimator)
+        stream.wait_stream(current)
+        result = _solve_on(estimator, estimator.dims, noise, mu, cond, spks, lengths, t_arr,
+                           dt_arr, n_steps, cfg_rate, streaming, use_graph, stream)
+        current.wait_stream(stream)
+        return result
+    offs = [0]
+    for n in lengths:
+        offs.append(offs[-1] + n)
+    # each group's rows, made on the caller's stream before the groups start
+    group_rows = [torch.cat([torch.arange(offs[i], offs[i + 1]) for i in g]).to(dev)
+                  for g in groups]
+    parts = []
+    streams = [_stream_for(r) for r in runners]
+    for s in streams:  # every group waits for the caller's work only, not for each other
+        s.wait_stream(current)
+    for runner, stream, g, rows in zip(runners, streams, groups, group_rows):
+        with torch.cuda.stream(stream):
+            out = _solve_on(runner, estimator.dims, noise[rows], mu[rows], cond[rows], spks[g],
+                            [lengths[i] for i in g], t_arr, dt_arr, n_steps, cfg_rate,
+                            streaming, use_graph, stream)
+            rows.record_stream(stream)
+        parts.append((rows, out))
+    for s in streams:
+        current.wait_stream(s)
+    result = torch.empty(rc, noise.shape[1], dtype=torch.float32, device=dev)
+    for rows, out in parts:
+        out.record_stream(current)
+        result[rows] = out
     return result
 
 

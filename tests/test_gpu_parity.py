@@ -130,6 +130,27 @@ def test_max_pos_document_among_many_tiny_ones(fcv, stress2, streaming):
     say(f"[limits] streaming={streaming} worst per-document rel_l2 {worst:.2e}")
 
 
+def test_concurrent_request_groups_equal_one_batch(fcv, stress2):
+    """The solve's request groups (each a packed CFG batch on its own handle and stream, all
+    in flight together) give the same rows as one packed batch, bit for bit: eager, first
+    graph capture and replay, for 1, 2, 3 and the default number of groups."""
+    _, est = stress2
+    lengths = [90, 300, 17, 150, 64, 33]
+    g = torch.Generator().manual_seed(23)
+    rc = sum(lengths)
+    noise, mu, cond = (torch.randn(rc, 80, generator=g) for _ in range(3))
+    spks = torch.randn(len(lengths), 80, generator=g)
+    solve = lambda c, graph: fcv.solve_euler_packed(est, noise, mu, cond, spks, lengths,
+                                                    n_steps=3, use_graph=graph,
+                                                    concurrency=c).cpu()
+    ref = solve(1, False)
+    for c in (2, 3, None):
+        for graph in (False, True, True, True):
+            say(f"[groups] concurrency={c} graph={graph}")
+            assert torch.equal(solve(c, graph), ref), f"concurrency {c}, graph {graph}"
+    assert fcv.solver.request_groups(lengths, 2) == [[1, 2], [0, 3, 4, 5]]
+
+
 def test_shared_t_equals_per_doc_t(fcv, stress2):
     """One shared t vs the same t per document.  Up to 4 t rows the time MLP and the AdaLN
     projection take the same bandwidth-bound path either way (bitwise equal); with more rows
