@@ -296,6 +296,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--groups", type=int, default=0,
+                    help="request groups the solve runs concurrently (0: the solver's default)")
     ap.add_argument("--workload", type=int, default=3, choices=[2, 3, 4, 5])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
@@ -345,7 +347,7 @@ def main() -> int:
 
     K = args.steps
 
-    def solve(graph: bool, concurrency: int | None = None):
+    def solve(graph: bool, concurrency: int | None = args.groups or None):
         return fcv.solve_euler_packed(est, batch.noise, batch.mu, batch.cond, batch.spks,
                                       batch.lengths, n_steps=K, streaming=batch.streaming,
                                       use_graph=graph, concurrency=concurrency)
@@ -453,7 +455,8 @@ def main() -> int:
             "rows_per_step": rows,
             "depth": 22, "dim": 1024, "heads": 16,
             "graph": "none (eager launches)" if args.eager else "hipGraph of the K-step solve",
-            "request_groups": len(fcv.solver.request_groups(batch.lengths, 2)),
+            "request_groups": len(fcv.solver.request_groups(
+                batch.lengths, args.groups or fcv.solver.default_concurrency(batch.n_requests))),
             "concurrency": ("requests split into cost-balanced groups, each a packed CFG batch "
                             "on its own handle and stream, all launched before any is waited "
                             "for; rows bit-identical to one packed batch"),

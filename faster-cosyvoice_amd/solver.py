@@ -57,6 +57,12 @@ def _stream_for(runner: _PackedRunner) -> torch.cuda.Stream:
     return runner._stream
 
 
+def default_concurrency(n_requests: int) -> int:
+    """Request groups a solve runs by default: two (measured best on one MI355X: config 3
+    -10 %, config 4 -7 %, config 5 even; three or four groups lose to smaller tiles)."""
+    return 2 if n_requests >= 2 else 1
+
+
 def request_groups(lengths: Sequence[int], n_groups: int) -> list[list[int]]:
     """Requests split into ``n_groups`` groups of about equal DiT cost, per request
     ``378 MFLOP x L + 90 kFLOP x L^2`` (dense rows, attention pairs), longest first onto the
@@ -119,7 +125,7 @@ def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.T
         raise ValueError(f"noise, mu and cond must hold {rc} rows")
     if spks.shape[0] != len(lengths):
         raise ValueError("spks must hold one row per request")
-    n_groups = (2 if len(lengths) >= 2 else 1) if concurrency is None else int(concurrency)
+    n_groups = default_concurrency(len(lengths)) if concurrency is None else int(concurrency)
     if n_groups < 1:
         raise ValueError("concurrency must be >= 1")
     groups = request_groups(lengths, n_groups)
