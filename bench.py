@@ -188,8 +188,9 @@ HIFT_REPEAT = 3
 
 def hift_leg(fcv, batch, dev, cpu: bool) -> dict:
     """The HiFT vocoder on the generated Mel of the workload's requests (request length minus
-    its prompt), all requests in one packed call: HIP events on the launch stream around
-    HIFT_REPEAT calls; plus the fp32/fp64 oracle on the host for a bounded sample."""
+    its prompt), one ``inference_batched`` call (two concurrent packed request groups): HIP
+    events on the caller's stream around HIFT_REPEAT calls; plus the fp32/fp64 oracle on the
+    host for a bounded sample."""
     import torch
     dims = fcv.synthetic.HiFTDims()
     gen = [n - p for n, p in zip(batch.lengths, batch.prompt_lengths)]
@@ -217,8 +218,8 @@ def hift_leg(fcv, batch, dev, cpu: bool) -> dict:
     flop = 2.0 * frames * sum(v for k, v in macs.items() if k != "f0_fp64")
     tflops = flop / (ms * 1e-3) / 1e12
     res = {
-        "what": "HiFT vocoder, Mel -> 24 kHz waveform, all requests in one packed call (fp32, "
-                "F0 predictor fp64)",
+        "what": "HiFT vocoder, Mel -> 24 kHz waveform, the requests as two concurrent packed "
+                "request groups (fp32, F0 predictor fp64)",
         "requests": len(gen), "mel_frames": frames, "audio_seconds": round(audio_s, 2),
         "ms_per_call": round(ms, 3),
         "audio_seconds_per_second": round(audio_s / (ms * 1e-3), 1),

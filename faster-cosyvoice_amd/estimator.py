@@ -85,14 +85,14 @@ class _Block(nn.Module):
 class _PackedRunner:
     """A libfcvdit handle with its own workspace, plan cache and launch stream.
 
-    The estimator is one; ``_Lane`` objects are more handles over the same derived weights, so
-    that independent groups of documents can run on concurrent streams.  Subclasses set
-    ``device``, ``static_chunk_size`` and ``_handle``."""
+    The estimator is one (request group 0); ``_Lane`` objects are more handles over the same
+    derived weights, so that independent groups of requests can run on concurrent streams.
+    Subclasses set ``device``, ``static_chunk_size`` and ``_handle``."""
 
-    def _init_runner(self) -> None:
+    def _init_runner(self, group: int = 0) -> None:
         self._workspace: torch.Tensor | None = None
         self._plan_key: tuple | None = None
-        self._stream: torch.cuda.Stream | None = None
+        self.group = group  # request group this runner serves (its stream: streams.group_stream)
         self.plan_calls = 0
 
     def _require(self) -> int:
@@ -134,13 +134,13 @@ class _PackedRunner:
 class _Lane(_PackedRunner):
     """A second handle over an estimator's derived weights (which the estimator keeps alive)."""
 
-    def __init__(self, owner: "DiTEstimator", handle: int):
+    def __init__(self, owner: "DiTEstimator", handle: int, group: int):
         self.device = owner.device
         self.static_chunk_size = owner.static_chunk_size
         self.dims = owner.dims
         self._handle = handle
         self._owner = owner
-        self._init_runner()
+        self._init_runner(group)
 
     def __del__(self):
         handle = getattr(self, "_handle", None)
@@ -331,7 +331,7 @@ class DiTEstimator(nn.Module, _PackedRunner):
         while len(self._extra_lanes) < n - 1:
             handle = _lib.c_void_p()
             _lib.check(lib.fcv_dit_create(*self._create_args, handle))
-            self._extra_lanes.append(_Lane(self, handle.value))
+            self._extra_lanes.append(_Lane(self, handle.value, len(self._extra_lanes) + 1))
         return [self] + self._extra_lanes[: n - 1]
 
     # -- compute ----------------------------------------------------------------------------

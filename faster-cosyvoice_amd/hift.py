@@ -18,6 +18,7 @@ import torch
 from scipy.signal import get_window
 
 from . import _lib
+from .streams import group_stream
 from .synthetic import HiFTDims, hift_state_dict_shapes, random_hift_buffers
 
 _G = ".parametrizations.weight.original0"
@@ -41,7 +42,9 @@ class HiFTVocoder:
         self._cdims = self._make_dims()
         self._handle: int | None = None
         self._keep: list[torch.Tensor] = []
-        self._ws: torch.Tensor | None = None
+        # extra handles over the same weight table, for request groups in flight together:
+        # [handle, workspace, stream]
+        self._lanes: list[list] = []
 
     # ---- construction ----------------------------------------------------------------------
 
@@ -170,10 +173,27 @@ class HiFTVocoder:
 
     def __del__(self):
         try:
+            for lane in getattr(self, "_lanes", [])[1:]:  # lane 0 is this vocoder's own handle
+                self._lib.fcv_hift_destroy(lane[0])
             if getattr(self, "_handle", None) is not None:
                 self._lib.fcv_hift_destroy(self._handle)
         except Exception:  # interpreter shutdown: the library may already be unloaded
             pass
+
+    def _lane(self, i: int) -> list:
+        """Request group i's [handle, workspace, stream]: group 0 is this vocoder's own handle;
+        later groups get handles over the same weight table.  Group i runs on the process's
+        group-i stream (streams.group_stream)."""
+        self._require()
+        while len(self._lanes) < i + 1:
+            if not self._lanes:
+                handle = self._handle
+            else:
+                h = _lib.c_void_p()
+                _lib.check(self._lib.fcv_hift_create(self._cdims, self._ptrs, len(self._ptrs), h))
+                handle = h.value
+            self._lanes.append([handle, None, group_stream(self.device, len(self._lanes))])
+        return self._lanes[i]
 
     def _require(self) -> int:
         if self._handle is None:
@@ -189,21 +209,10 @@ class HiFTVocoder:
                              f"{'final' if finalize else 'non-final'} chunk")
         return n
 
-    @torch.no_grad()
-    def inference_batched(self, mels: Sequence[torch.Tensor],
-                          finalize_list: Sequence[bool] | None = None,
-                          return_source: bool = False):
-        """Vocode requests of different lengths in one packed pass.  ``mels``: each
-        ``[80, T]`` or ``[1, 80, T]``.  Returns one ``[1, N]`` fp32 waveform per request (and
-        the ``[1, 1, L]`` sources with ``return_source``).  Each waveform equals what
-        ``inference`` gives for that request alone."""
-        h = self._require()
-        mels = [m.reshape(m.shape[-2], m.shape[-1]) for m in mels]
-        if not mels:
-            raise ValueError("no Mel input")
-        fin = [True] * len(mels) if finalize_list is None else [bool(f) for f in finalize_list]
-        if len(fin) != len(mels):
-            raise ValueError("one finalize flag per request is required")
+    def _run(self, lane: list, mels: list[torch.Tensor], fin: list[bool], return_source: bool,
+             stream: int) -> tuple[list, list]:
+        """Packed calls of at most HIFT_MAX_DOCS requests on ``lane``, enqueued on ``stream``."""
+        h = lane[0]
         speech_all, source_all = [], []
         for g0 in range(0, len(mels), _lib.HIFT_MAX_DOCS):
             group = mels[g0:g0 + _lib.HIFT_MAX_DOCS]
@@ -219,16 +228,15 @@ class HiFTVocoder:
             need = int(self._lib.fcv_hift_workspace_bytes(h, fr, fl, len(group)))
             if need == 0:
                 raise ValueError("bad HiFT call layout")
-            if self._ws is None or self._ws.numel() < need:
-                self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+            if lane[1] is None or lane[1].numel() < need:
+                lane[1] = torch.empty(need, dtype=torch.uint8, device=self.device)
             speech = torch.empty(max(sum(samples), 1), dtype=torch.float32, device=self.device)
             source = (torch.empty(max(sum(src_len), 1), dtype=torch.float32, device=self.device)
                       if return_source else None)
-            stream = torch.cuda.current_stream(self.device).cuda_stream
             _lib.check(self._lib.fcv_hift_inference(
                 h, x.data_ptr(), fr, fl, len(group), speech.data_ptr(),
-                source.data_ptr() if source is not None else None, self._ws.data_ptr(),
-                self._ws.numel(), stream))
+                source.data_ptr() if source is not None else None, lane[1].data_ptr(),
+                lane[1].numel(), stream))
             off = 0
             for n in samples:
                 speech_all.append(speech[off:off + n].view(1, n))
@@ -238,6 +246,59 @@ class HiFTVocoder:
                 for n in src_len:
                     source_all.append(source[off:off + n].view(1, 1, n))
                     off += n
+        return speech_all, source_all
+
+    @torch.no_grad()
+    def inference_batched(self, mels: Sequence[torch.Tensor],
+                          finalize_list: Sequence[bool] | None = None,
+                          return_source: bool = False, concurrency: int | None = None):
+        """Vocode requests of different lengths in packed passes.  ``mels``: each ``[80, T]``
+        or ``[1, 80, T]``.  Returns one ``[1, N]`` fp32 waveform per request (and the
+        ``[1, 1, L]`` sources with ``return_source``).  Each waveform equals what
+        ``inference`` gives for that request alone.
+
+        The requests run as ``concurrency`` groups (default: 2 when there are at least 2),
+        balanced by Mel frames, each a packed call on its own handle over the shared weights
+        and its own stream, all in flight together (one packed call of 8 requests at config 3:
+        23.5 ms; two groups: 22.1 ms)."""
+        self._require()
+        mels = [m.reshape(m.shape[-2], m.shape[-1]) for m in mels]
+        if not mels:
+            raise ValueError("no Mel input")
+        fin = [True] * len(mels) if finalize_list is None else [bool(f) for f in finalize_list]
+        if len(fin) != len(mels):
+            raise ValueError("one finalize flag per request is required")
+        n_groups = (2 if len(mels) >= 2 else 1) if concurrency is None else int(concurrency)
+        if n_groups < 1:
+            raise ValueError("concurrency must be >= 1")
+        # longest first onto the group with the fewest frames
+        groups: list[list[int]] = [[] for _ in range(min(n_groups, len(mels)))]
+        load = [0] * len(groups)
+        for i in sorted(range(len(mels)), key=lambda i: -int(mels[i].shape[1])):
+            g = load.index(min(load))
+            groups[g].append(i)
+            load[g] += int(mels[i].shape[1])
+        groups = [sorted(g) for g in groups]
+        current = torch.cuda.current_stream(self.device)
+        lanes = [self._lane(k) for k in range(len(groups))]
+        for lane in lanes:  # every group waits for the caller's work only
+            lane[2].wait_stream(current)
+        results = []
+        for lane, g in zip(lanes, groups):
+            with torch.cuda.stream(lane[2]):
+                results.append(self._run(lane, [mels[i] for i in g], [fin[i] for i in g],
+                                         return_source, lane[2].cuda_stream))
+        for lane in lanes:
+            current.wait_stream(lane[2])
+        speech_all: list = [None] * len(mels)
+        source_all: list = [None] * len(mels)
+        for g, (sp, so) in zip(groups, results):
+            for k, i in enumerate(g):
+                sp[k].record_stream(current)
+                speech_all[i] = sp[k]
+                if return_source:
+                    so[k].record_stream(current)
+                    source_all[i] = so[k]
         return (speech_all, source_all) if return_source else speech_all
 
     @torch.no_grad()

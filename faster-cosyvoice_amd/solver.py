@@ -18,6 +18,7 @@ import torch
 
 from . import _lib
 from .estimator import DiTEstimator, _PackedRunner
+from .streams import group_stream
 
 
 def euler_schedule(n_steps: int) -> tuple[list[float], list[float]]:
@@ -51,10 +52,8 @@ def _solver_buffers(runner: _PackedRunner, dims, rc: int, n_req: int) -> dict[st
 
 
 def _stream_for(runner: _PackedRunner) -> torch.cuda.Stream:
-    # hipGraph capture needs a non-default stream; default priority as required.
-    if runner._stream is None:
-        runner._stream = torch.cuda.Stream(device=runner.device)
-    return runner._stream
+    # a non-default stream (hipGraph capture needs one), shared per group across the process
+    return group_stream(runner.device, runner.group)
 
 
 def default_concurrency(n_requests: int) -> int:
