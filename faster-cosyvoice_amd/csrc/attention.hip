@@ -91,29 +91,34 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
       qf[ks] = *reinterpret_cast<const bf16x8*>(Qh + (long)qr * HD + ks * 16 + hl * 8);
   }
 
-  // tile loaders: each thread moves 2 x 16 bytes of K and 2 x 16 bytes of V^T
+  // tile loaders: each thread moves 2 x 16 bytes of K and 2 x 16 bytes of V^T.  A V^T chunk
+  // holds 8 keys from a multiple of 8 (documents start 8-aligned, the pitch rp is a multiple of
+  // 8), so a chunk that holds a key below kv_end lies inside the row; keys at or past kv_end
+  // are zeroed when the chunk is stashed.  Loads are always full vectors and the next tile is
+  // fetched unconditionally (addresses clamped; the surplus tile lands in the buffer no later
+  // iteration reads), so the compiler never waits on a load before the stash that consumes it.
   const int lr = tid >> 3;         // 0..31
   const int lc = (tid & 7) * 8;    // 0..56
   bf16x8 rk[2], rv[2];
+  int vcnt = 8;  // keys of this thread's V^T chunks below kv_end
   auto fetch = [&](int kb) {
+    const int k0 = kb + lc;
+    vcnt = kv_end - k0;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      int key = min(kb + lr + 32 * i, rows - 1);
+      const int key = min(kb + lr + 32 * i, rows - 1);
       rk[i] = *reinterpret_cast<const bf16x8*>(Kh + (long)key * HD + lc);
       const int d = lr + 32 * i;
-      const int k0 = kb + lc;
-      const bf16* src = Vh + (long)d * rp + k0;
-      if (k0 + 8 <= kv_end) {
-        rv[i] = *reinterpret_cast<const bf16x8*>(src);
-      } else {
-        bf16x8 t;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) t[e] = (k0 + e < kv_end) ? src[e] : f2bf(0.0f);
-        rv[i] = t;
-      }
+      rv[i] = *reinterpret_cast<const bf16x8*>(Vh + (long)d * rp + min(k0, rp - 8));
     }
   };
   auto stash = [&](int buf) {
+    if (vcnt < 8) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rv[i][e] = e < vcnt ? rv[i][e] : f2bf(0.0f);
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       *reinterpret_cast<bf16x8*>(&sK[buf][lr + 32 * i][lc]) = rk[i];
@@ -142,7 +147,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
   for (int it = 0; it < n_kt; ++it) {
     const int cur = it & 1;
     const int kb = kv_begin + it * TK;
-    if (it + 1 < n_kt) fetch(kb + TK);
+    fetch(kb + TK);
 
     // S^T[key][query] for two 32-key halves (raw q.k)
     f32x16 s[2];
@@ -215,7 +220,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
       }
     }
 
-    if (it + 1 < n_kt) stash(cur ^ 1);
+    stash(cur ^ 1);
     __syncthreads();
   }
 
