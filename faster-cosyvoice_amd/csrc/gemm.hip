@@ -131,7 +131,8 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   const int m0 = tmi * BM;
   const int n0 = tni * BN;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave index as a scalar, so the copies' LDS destinations are computed in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm0 = (wave / C::WN) * (BM / C::WM);
   const int wn0 = (wave % C::WN) * (BN / C::WN);
 
@@ -194,8 +195,9 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   const int fr = lane & 31, fh = lane >> 5;
   // Ring of S stages.  Iteration kt: wait for this wave's copies of slice kt (the copies of
   // the up to S-2 later slices already issued may still be in flight; loads complete in order),
-  // barrier (all copies of slice kt landed, every wave done reading slice kt-1), start slice
-  // kt+S-1 into the stage slice kt-1 used, then run slice kt's MFMAs.  Inside a slice the
+  // barrier (all copies of slice kt landed, every wave done reading slice kt-1), read k-step 0's
+  // fragments, start slice kt+S-1 into the stage slice kt-1 used (its address arithmetic runs
+  // while the fragment reads are in flight), then run slice kt's MFMAs.  Inside a slice the
   // fragments of k-step ks+1 are read from LDS while the MFMAs of k-step ks run.
   const int KT = K / BK;
 #pragma unroll
@@ -206,7 +208,6 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
     // slices issued after slice kt: min(S - 2, KT - 1 - kt)
     wait_loads_ahead<C::LOADS, S - 2>(KT - 1 - kt);
     __syncthreads();
-    if (kt + S - 1 < KT) issue(kt + S - 1, stage == 0 ? S - 1 : stage - 1);
     const bf16* a_st = sA[stage];
     const bf16* b_st = sB[stage];
     bf16x8 fa[2][TM], fb[2][TN];
@@ -224,6 +225,8 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
       }
     };
     load(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + S - 1 < KT) issue(kt + S - 1, stage == 0 ? S - 1 : stage - 1);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       // scheduling fences keep k-step ks+1's LDS reads ahead of k-step ks's MFMAs (left alone,
