@@ -88,7 +88,12 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
   const bf16x8 zero8 = {};
   for (int j = 0; j < taps; ++j) {
     const int cur = j & 1;
-    if (j + 1 < taps) fetch(j + 1);
+    // the next tap's weights are fetched and stashed unconditionally (the last tap re-reads
+    // its own slice into the idle buffer), so no path leaves the fetch pending and the compiler
+    // does not wait for it before this tap's MFMAs; the fence keeps the loads at the top of the
+    // tap (left alone, the scheduler sinks them next to the stash and waits on them there)
+    fetch(min(j + 1, taps - 1));
+    __builtin_amdgcn_sched_barrier(0);
     // rows before the row's document start read as zero (per-document causal padding)
     const bool live = lpos + j >= halo;
 #pragma unroll
@@ -101,7 +106,7 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
         acc[t] = mfma32(wa, xb, acc[t]);
       }
     }
-    if (j + 1 < taps) stash(cur ^ 1);
+    stash(cur ^ 1);
     __syncthreads();
   }
 
