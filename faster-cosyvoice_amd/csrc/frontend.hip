@@ -117,9 +117,13 @@ __global__ __launch_bounds__(256) void lookahead_conv1_kernel(
   fetch(0);
   stash(0);
   __syncthreads();
+  // the next chunk is fetched and stashed unconditionally (clamped to the last chunk; the
+  // surplus lands in the buffer no later iteration reads), so the compiler does not wait for
+  // the fetch before this chunk's MFMAs; the fence keeps the fetch at the top
   for (int kc = 0; kc < KC; ++kc) {
     const int cur = kc & 1;
-    if (kc + 1 < KC) fetch(kc + 1);
+    fetch(min(kc + 1, KC - 1));
+    __builtin_amdgcn_sched_barrier(0);
     f32x4 av[4], bv[2];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
@@ -133,7 +137,7 @@ __global__ __launch_bounds__(256) void lookahead_conv1_kernel(
       for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b) acc[a][b] = mfma16(av[a][s], bv[b][s], acc[a][b]);
-    if (kc + 1 < KC) stash(cur ^ 1);
+    stash(cur ^ 1);
     __syncthreads();
   }
 
@@ -212,7 +216,8 @@ __global__ __launch_bounds__(256) void lookahead_conv2_kernel(
   __syncthreads();
   for (int kc = kc_begin; kc < kc_end; ++kc) {
     const int cur = (kc - kc_begin) & 1;
-    if (kc + 1 < kc_end) fetch(kc + 1);
+    fetch(min(kc + 1, kc_end - 1));  // unconditional, as in the first layer's loop
+    __builtin_amdgcn_sched_barrier(0);
     f32x4 av[OT];
 #pragma unroll
     for (int a = 0; a < OT; ++a)
@@ -222,7 +227,7 @@ __global__ __launch_bounds__(256) void lookahead_conv2_kernel(
     for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int a = 0; a < OT; ++a) acc[a] = mfma16(av[a][s], bv[s], acc[a]);
-    if (kc + 1 < kc_end) stash(cur ^ 1);
+    stash(cur ^ 1);
     __syncthreads();
   }
 

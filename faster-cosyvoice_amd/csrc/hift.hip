@@ -176,20 +176,26 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const 
   };
 
   fetch(0, ra[0], rb[0]);
-  if (KC > 1) fetch(1, ra[1], rb[1]);
+  fetch(min(1, KC - 1), ra[1], rb[1]);
   stash(0, ra[0], rb[0]);
   __syncthreads();
+  // Fetches and stashes run unconditionally (chunk indices clamped to the last chunk; a surplus
+  // chunk lands in the LDS buffer no later computation reads), so no path leaves a load
+  // pending and the compiler does not wait for the loads before the computation they overlap.
+  // The fences keep each fetch ahead of its computation.
   for (int kc = 0; kc < KC; kc += 2) {
     // chunk kc is in LDS buffer 0; register set 1 holds chunk kc + 1
-    if (kc + 2 < KC) fetch(kc + 2, ra[0], rb[0]);
+    fetch(min(kc + 2, KC - 1), ra[0], rb[0]);
+    __builtin_amdgcn_sched_barrier(0);
     compute(0);
-    if (kc + 1 < KC) stash(1, ra[1], rb[1]);
+    stash(1, ra[1], rb[1]);
     __syncthreads();
     if (kc + 1 >= KC) break;
     // chunk kc + 1 is in buffer 1; register set 0 holds chunk kc + 2
-    if (kc + 3 < KC) fetch(kc + 3, ra[1], rb[1]);
+    fetch(min(kc + 3, KC - 1), ra[1], rb[1]);
+    __builtin_amdgcn_sched_barrier(0);
     compute(1);
-    if (kc + 2 < KC) stash(0, ra[0], rb[0]);
+    stash(0, ra[0], rb[0]);
     __syncthreads();
   }
 
