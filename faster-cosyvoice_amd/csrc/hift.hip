@@ -400,9 +400,6 @@ __global__ __launch_bounds__(256) void istft_ola_kernel(const float* __restrict_
 
 unsigned blocks_for(long n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
-
-
-
 template <typename T>
 hipError_t launch_conv(const HiftConv& p, const HiftDocs& docs, hipStream_t stream) {
   if (p.rows_out <= 0) return hipSuccess;
