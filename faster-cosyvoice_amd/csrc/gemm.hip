@@ -79,18 +79,20 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   return BK == 64 ? chunk ^ ((row >> 1) & 7) : chunk ^ ((row >> 2) & 3);
 }
 
-// Lane-strided 16-byte global -> LDS copy: lane l writes bytes [16 l, 16 l + 16) of `dst`
-// (dst wave-uniform).  Issued as inline asm so the compiler does not treat every later LDS read
-// as dependent on it (it would wait for vmcnt(0) before each one); the K loop orders these copies
-// with explicit vmcnt waits and barriers instead.
-// (m0 is named as a clobber on purpose: the copy's LDS base lives there.)
+// Lane-strided 16-byte global -> LDS copy: lane l copies the 16 bytes at base + voff (its own
+// 32-bit byte offset from a wave-uniform 64-bit base held in SGPRs) to bytes [16 l, 16 l + 16)
+// from the wave-uniform LDS address `lds`.  With the base and the LDS address scalar, a copy
+// costs one m0 write and one load instruction; the K advance is a scalar add on the base.
+// Issued as inline asm so the compiler does not treat every later LDS read as dependent on it
+// (it would wait for vmcnt(0) before each one); the K loop orders these copies with explicit
+// vmcnt waits and barriers instead.  (m0 is named as a clobber on purpose: the copy's LDS base
+// lives there.)
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(const bf16* src, bf16* dst) {
-  const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)dst;
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
-               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(src)
+               : "s"(lds), "v"(voff), "s"(base)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -137,29 +139,35 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   const int wn0 = (wave % C::WN) * (BN / C::WN);
 
   // per-lane source of each copy: row r0 + lane / ROW_CHUNKS, and the chunk that belongs at LDS
-  // position lane % ROW_CHUNKS of that row (A rows clamped to M - 1)
+  // position lane % ROW_CHUNKS of that row (A rows clamped to M - 1), as a byte offset from the
+  // operand's base (A spans < 4 GB: rows x lda x 2 bytes).  The destinations are scalar: the
+  // stage's base + this wave's first copy row + i copies.
   const int lrow = lane / C::ROW_CHUNKS;
   const int lpos = lane % C::ROW_CHUNKS;
-  const bf16* a_src[C::A_INSTR];
-  const bf16* w_src[C::B_INSTR];
+  uint32_t a_off[C::A_INSTR], w_off[C::B_INSTR];
 #pragma unroll
   for (int i = 0; i < C::A_INSTR; ++i) {
     const int row = (wave * C::A_INSTR + i) * C::ROWS_PER_COPY + lrow;
-    a_src[i] = A + (long)min(m0 + row, M - 1) * lda + swz<BK>(row, lpos) * 8;
+    a_off[i] = (uint32_t)(((long)min(m0 + row, M - 1) * lda + swz<BK>(row, lpos) * 8) * 2);
   }
 #pragma unroll
   for (int i = 0; i < C::B_INSTR; ++i) {
     const int row = (wave * C::B_INSTR + i) * C::ROWS_PER_COPY + lrow;
-    w_src[i] = W + (long)(n0 + row) * ldw + swz<BK>(row, lpos) * 8;
+    w_off[i] = (uint32_t)(((long)(n0 + row) * ldw + swz<BK>(row, lpos) * 8) * 2);
   }
+  constexpr uint32_t kCopyBytes = C::ROWS_PER_COPY * BK * 2;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)smem;
+  const uint32_t lds_a = lds_base + (uint32_t)wave * C::A_INSTR * kCopyBytes;
+  const uint32_t lds_b = lds_base + S * BM * BK * 2 + (uint32_t)wave * C::B_INSTR * kCopyBytes;
   auto issue = [&](int kt, int stage) {
-    const int koff = kt * BK;
+    const bf16* a_k = A + kt * BK;
+    const bf16* w_k = W + kt * BK;
 #pragma unroll
     for (int i = 0; i < C::A_INSTR; ++i)
-      lds_dma16(a_src[i] + koff, &sA[stage][(wave * C::A_INSTR + i) * C::ROWS_PER_COPY * BK]);
+      lds_dma16(a_k, a_off[i], lds_a + stage * (BM * BK * 2) + i * kCopyBytes);
 #pragma unroll
     for (int i = 0; i < C::B_INSTR; ++i)
-      lds_dma16(w_src[i] + koff, &sB[stage][(wave * C::B_INSTR + i) * C::ROWS_PER_COPY * BK]);
+      lds_dma16(w_k, w_off[i], lds_b + stage * (BN * BK * 2) + i * kCopyBytes);
   };
 
   // Column-only epilogue inputs (bias; gates shared by all rows) are loaded here, before the K
@@ -593,6 +601,8 @@ hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, 
                   const Epi& epi, hipStream_t stream) {
   if (M <= 0) return hipSuccess;
   if (N % 128 != 0 || K % 64 != 0 || lda % 8 != 0 || ldw % 8 != 0) return hipErrorInvalidValue;
+  // the copies address A and W by 32-bit byte offsets from their bases
+  if ((long)M * lda * 2 >= (1L << 32) || (long)N * ldw * 2 >= (1L << 32)) return hipErrorInvalidValue;
   switch (choose_tile(M, N)) {
     case 0: return launch_tile<Tile256x256>(A, lda, W, ldw, M, N, K, epi, stream);
     case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream);
