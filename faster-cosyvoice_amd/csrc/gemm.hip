@@ -201,54 +201,74 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
   const int fr = lane & 31, fh = lane >> 5;
-  // Ring of S stages.  Iteration kt: wait for this wave's copies of slice kt (the copies of
-  // the up to S-2 later slices already issued may still be in flight; loads complete in order),
-  // barrier (all copies of slice kt landed, every wave done reading slice kt-1), read k-step 0's
-  // fragments, start slice kt+S-1 into the stage slice kt-1 used (its address arithmetic runs
-  // while the fragment reads are in flight), then run slice kt's MFMAs.  Inside a slice the
-  // fragments of k-step ks+1 are read from LDS while the MFMAs of k-step ks run.
+  // Ring of S stages, K loop rotated by one k-step.  Slice j is published by a wait for this
+  // wave's copies of slice j (the copies of the up to S-2 later slices already issued may still
+  // be in flight; loads complete in order) and a barrier (all copies of slice j landed; every
+  // wave has its last fragments of slice j-1 in registers, so the stage slice j-1 used is free).
+  // The barrier sits between k-steps KS-2 and KS-1 of slice j-1: after it the wave starts slice
+  // j+S-1 into that free stage, reads slice j's k-step 0 fragments, and runs slice j-1's last
+  // k-step from registers while those reads are in flight, so the matrix pipe does not wait on
+  // a fresh LDS read after a barrier.  Inside a slice the fragments of k-step ks+1 are read
+  // while the MFMAs of k-step ks run.  Every accumulator sees its k-steps in the same order as
+  // an unrotated loop.
   const int KT = K / BK;
+  constexpr int KS = BK / 16;
+  static_assert(KS % 2 == 0, "k-step 0 of a slice uses fragment buffer 0");
+  bf16x8 fa[2][TM], fb[2][TN];
+  auto load = [&](int buf, int ks, int st) {
+    const bf16* a_st = sA[st];
+    const bf16* b_st = sB[st];
+    const int chunk = ks * 2 + fh;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row = wm0 + i * 32 + fr;
+      fa[buf][i] = *reinterpret_cast<const bf16x8*>(a_st + row * BK + swz<BK>(row, chunk) * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int row = wn0 + j * 32 + fr;
+      fb[buf][j] = *reinterpret_cast<const bf16x8*>(b_st + row * BK + swz<BK>(row, chunk) * 8);
+    }
+  };
+  // scheduling fences keep each k-step's LDS reads ahead of the previous k-step's MFMAs (left
+  // alone, the scheduler sinks each read next to its first use and waits on it)
+  auto mma = [&](int buf) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(fb[buf][j], fa[buf][i], acc[i][j]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // k-steps 0 .. KS-2 of the slice in stage st (k-step 0's fragments already in buffer 0);
+  // leaves k-step KS-1's fragments in buffer 1
+  auto slice_head = [&](int st) {
+#pragma unroll
+    for (int ks = 0; ks + 1 < KS; ++ks) {
+      load((ks + 1) & 1, ks + 1, st);
+      mma(ks & 1);
+    }
+  };
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
     if (st < KT) issue(st, st);
+  wait_loads_ahead<C::LOADS, S - 2>(KT - 1);  // slice 0
+  __syncthreads();
+  if (S - 1 < KT) issue(S - 1, S - 1);
+  load(0, 0, 0);
+  slice_head(0);
   int stage = 0;
-  for (int kt = 0; kt < KT; ++kt) {
-    // slices issued after slice kt: min(S - 2, KT - 1 - kt)
-    wait_loads_ahead<C::LOADS, S - 2>(KT - 1 - kt);
+  for (int kt = 1; kt < KT; ++kt) {
+    const int next = stage == S - 1 ? 0 : stage + 1;
+    wait_loads_ahead<C::LOADS, S - 2>(KT - 1 - kt);  // slice kt
     __syncthreads();
-    const bf16* a_st = sA[stage];
-    const bf16* b_st = sB[stage];
-    bf16x8 fa[2][TM], fb[2][TN];
-    auto load = [&](int buf, int ks) {
-      const int chunk = ks * 2 + fh;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int row = wm0 + i * 32 + fr;
-        fa[buf][i] = *reinterpret_cast<const bf16x8*>(a_st + row * BK + swz<BK>(row, chunk) * 8);
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int row = wn0 + j * 32 + fr;
-        fb[buf][j] = *reinterpret_cast<const bf16x8*>(b_st + row * BK + swz<BK>(row, chunk) * 8);
-      }
-    };
-    load(0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    if (kt + S - 1 < KT) issue(kt + S - 1, stage == 0 ? S - 1 : stage - 1);
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      // scheduling fences keep k-step ks+1's LDS reads ahead of k-step ks's MFMAs (left alone,
-      // the scheduler sinks each read next to its first use and waits on it)
-      if (ks + 1 < BK / 16) load((ks + 1) & 1, ks + 1);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(fb[ks & 1][j], fa[ks & 1][i], acc[i][j]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    stage = stage == S - 1 ? 0 : stage + 1;
+    if (kt + S - 1 < KT) issue(kt + S - 1, stage);  // into the stage slice kt-1 used
+    load(0, 0, next);
+    mma(1);  // slice kt-1, last k-step
+    slice_head(next);
+    stage = next;
   }
+  mma(1);  // last slice, last k-step
 
   // Nothing is in flight here; the explicit wait tells the compiler's counter tracking that the
   // column loads issued before the loop are complete on every path (with a zero-trip loop path
