@@ -589,18 +589,18 @@ hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, in
   return hipGetLastError();
 }
 
-// Tile choice: estimated time = (tiles per CU, rounded up) x tile area / per-CU rate, with the
-// rates measured for each shape at large M with the production epilogues (128x128 runs two
-// workgroups per CU, which its rate includes; 32x128 is rated low so it only wins when the
-// larger shapes leave most CUs idle, as for the 128-column output projection; 160x256 (four
-// waves of 160x64) fills 232 of the 256 CUs for the 1024-column GEMMs of a ~9k-row batch,
-// where 192x256 fills 196).  The choice only changes which rows and columns
-// share a workgroup: every output element still accumulates its K slices in the same order, so
-// results are bitwise identical for every tile shape (batch invariance holds).
+// Tile choice: estimated time = (tiles per CU, rounded up) x tile area / per-CU rate.  The
+// rates are fitted so the estimate picks the fastest shape measured for the block GEMMs
+// (N = 1024, 2048, 3072 at ~4.6k and ~9.2k rows, production epilogues): 128x128 runs two
+// workgroups per CU, which its rate includes; 160x256 runs one wave per SIMD, so it rates low
+// although it fills more CUs; 32x128 is rated low so it only wins when the larger shapes leave
+// most CUs idle, as for the 128-column output projection.  The choice only changes which rows
+// and columns share a workgroup: every output element still accumulates its K slices in the
+// same order, so results are bitwise identical for every tile shape (batch invariance holds).
 constexpr int kCus = 256;
 constexpr int kTileShape[7][2] = {{256, 256}, {192, 256}, {128, 256}, {256, 128}, {128, 128},
                                    {32, 128}, {160, 256}};
-constexpr float kTileRate[7] = {1.0f, 0.97f, 0.88f, 0.81f, 0.87f, 0.45f, 0.85f};
+constexpr float kTileRate[7] = {1.0f, 0.97f, 0.80f, 0.78f, 0.85f, 0.45f, 0.75f};
 
 inline int choose_tile(int M, int N) {
   int best = 4;
