@@ -364,6 +364,29 @@ __device__ __forceinline__ float4 add4(const f32x4& v, const float4& b) {
 struct NoCtx {};
 struct BiasCol { float4 b; };
 
+// Raw buffer accesses (stride 0) over [base, base + bytes): a load past `bytes` reads zeros and a
+// store past it is dropped, so row guards (row >= M) cost no branch, and the offsets are 32-bit
+// (the callers' M x ld x element size stays below 4 GB).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float4 buffer_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return float4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
+                __uint_as_float(v.w)};
+}
+__device__ __forceinline__ void buffer_st4(__amdgpu_buffer_rsrc_t r, uint32_t off, float4 x) {
+  const u32x4 v = {__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z),
+                   __float_as_uint(x.w)};
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
+}
+__device__ __forceinline__ void buffer_st_bf16x4(__amdgpu_buffer_rsrc_t r, uint32_t off, bf16x4 x) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, x), r, off, 0, 0);
+}
+
 struct EpiBiasF32Bf16 {
   const float* bias;
   float* out_f32;
@@ -464,17 +487,20 @@ struct EpiBiasGeluBf16 {
     const float4 y = add4(v, c.b);
     const bf16x4 yb = {f2bf(gelu_tanh(y.x)), f2bf(gelu_tanh(y.y)), f2bf(gelu_tanh(y.z)),
                        f2bf(gelu_tanh(y.w))};
-    if (row >= M) return;
-    *reinterpret_cast<bf16x4*>(out + (long)row * ldo + col) = yb;
+    buffer_st_bf16x4(buffer_over(out, (uint32_t)M * ldo * 2), (uint32_t)(row * ldo + col) * 2, yb);
   }
 };
 
+// h += gate * (acc + bias).  kPerDoc: each document has its own gate row (gate + d * mod_stride,
+// d = docid[row]); otherwise one gate row is shared by every document and is loaded with the
+// bias, before the K loop.  h is read and written through raw buffer accesses over its M rows.
+template <bool kPerDoc>
 struct EpiGatedResidual {
   const float* bias;
   float* h;
   int ldh;
   const float* gate;  // mod + gate offset
-  long mod_stride;    // 0: one gate row shared by every document
+  long mod_stride;
   const int32_t* docid;
   struct Col { float4 b, g; };
   struct Ctx { float4 g, x; };
@@ -484,25 +510,23 @@ struct EpiGatedResidual {
   __device__ Col column(int col) const {
     Col c;
     c.b = ld4(bias + col);
-    c.g = mod_stride == 0 ? ld4(gate + col) : float4{0.f, 0.f, 0.f, 0.f};
+    c.g = kPerDoc ? float4{0.f, 0.f, 0.f, 0.f} : ld4(gate + col);
     return c;
   }
   __device__ Ctx prepare(int row, int col, int M, const Col& c) const {
     Ctx x;
     x.g = c.g;
-    x.x = float4{0.f, 0.f, 0.f, 0.f};
-    if (row < M) {
-      if (mod_stride != 0) x.g = ld4(gate + (long)docid[row] * mod_stride + col);
-      x.x = ld4(h + (long)row * ldh + col);
+    if constexpr (kPerDoc) {
+      if (row < M) x.g = ld4(gate + (long)docid[row] * mod_stride + col);
     }
+    x.x = buffer_ld4(buffer_over(h, (uint32_t)M * ldh * 4), (uint32_t)(row * ldh + col) * 4);
     return x;
   }
   __device__ void finish(const f32x4& v, const Ctx& x, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
     const float4 r = {x.x.x + x.g.x * y.x, x.x.y + x.g.y * y.y, x.x.z + x.g.z * y.z,
                       x.x.w + x.g.w * y.w};
-    if (row >= M) return;
-    *reinterpret_cast<float4*>(h + (long)row * ldh + col) = r;
+    buffer_st4(buffer_over(h, (uint32_t)M * ldh * 4), (uint32_t)(row * ldh + col) * 4, r);
   }
 };
 
@@ -669,14 +693,19 @@ hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, c
 
 hipError_t gemm_bias_gelu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, bf16* out, int ldo, hipStream_t stream) {
+  if ((long)M * ldo * 2 >= (1L << 32)) return hipErrorInvalidValue;  // 32-bit buffer offsets
   return launch(A, lda, W, ldw, M, N, K, EpiBiasGeluBf16{bias, out, ldo}, stream);
 }
 
 hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, float* h, int ldh, const float* gate,
                                long mod_stride, const int32_t* docid, hipStream_t stream) {
+  if ((long)M * ldh * 4 >= (1L << 32)) return hipErrorInvalidValue;  // 32-bit buffer offsets
+  if (mod_stride == 0)
+    return launch(A, lda, W, ldw, M, N, K,
+                  EpiGatedResidual<false>{bias, h, ldh, gate, 0, docid}, stream);
   return launch(A, lda, W, ldw, M, N, K,
-                EpiGatedResidual{bias, h, ldh, gate, mod_stride, docid}, stream);
+                EpiGatedResidual<true>{bias, h, ldh, gate, mod_stride, docid}, stream);
 }
 
 hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const float* bias, int M,
