@@ -91,14 +91,20 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
       qf[ks] = *reinterpret_cast<const bf16x8*>(Qh + (long)qr * HD + ks * 16 + hl * 8);
   }
 
-  // tile loaders: each thread moves 2 x 16 bytes of K and 2 x 16 bytes of V^T.  A V^T chunk
-  // holds 8 keys from a multiple of 8 (documents start 8-aligned, the pitch rp is a multiple of
-  // 8), so a chunk that holds a key below kv_end lies inside the row; keys at or past kv_end
-  // are zeroed when the chunk is stashed.  Loads are always full vectors and the next tile is
-  // fetched unconditionally (addresses clamped; the surplus tile lands in the buffer no later
-  // iteration reads), so the compiler never waits on a load before the stash that consumes it.
+  // tile loaders: each thread moves 2 x 16 bytes of K and 2 x 16 bytes of V^T, through raw
+  // buffer loads over this head's K rows and V^T block: 32-bit offsets, and chunks past the end
+  // read as zeros (keys past `rows` are masked anyway).  A V^T chunk holds 8 keys from a
+  // multiple of 8 (documents start 8-aligned); keys at or past kv_end are zeroed when the chunk
+  // is stashed.  The next tile is fetched unconditionally (the surplus tile lands in the buffer
+  // no later iteration reads), so the compiler never waits on a load before the stash that
+  // consumes it.
   const int lr = tid >> 3;         // 0..31
   const int lc = (tid & 7) * 8;    // 0..56
+  const __amdgpu_buffer_rsrc_t k_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(Kh), (short)0, rows * HD * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(Vh), (short)0, HD * rp * 2, 0x00020000);
+  const uint32_t k_lane = (uint32_t)(lr * HD + lc) * 2, v_lane = (uint32_t)(lr * rp) * 2;
   bf16x8 rk[2], rv[2];
   int vcnt = 8;  // keys of this thread's V^T chunks below kv_end
   auto fetch = [&](int kb) {
@@ -106,10 +112,12 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
     vcnt = kv_end - k0;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int key = min(kb + lr + 32 * i, rows - 1);
-      rk[i] = *reinterpret_cast<const bf16x8*>(Kh + (long)key * HD + lc);
-      const int d = lr + 32 * i;
-      rv[i] = *reinterpret_cast<const bf16x8*>(Vh + (long)d * rp + min(k0, rp - 8));
+      rk[i] = __builtin_bit_cast(
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                      k_rsrc, k_lane + (uint32_t)(kb + 32 * i) * HD * 2, 0, 0));
+      rv[i] = __builtin_bit_cast(
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                      v_rsrc, v_lane + (uint32_t)(32 * i * rp + k0) * 2, 0, 0));
     }
   };
   auto stash = [&](int buf) {
@@ -248,6 +256,9 @@ hipError_t attention_varlen(const bf16* q, const bf16* k, const bf16* vt, bf16* 
                             const int32_t* tiles, int n_tiles, int rows, int rp, int heads,
                             int chunk, hipStream_t stream) {
   if (n_tiles <= 0) return hipSuccess;
+  // per-head K rows and V^T blocks are addressed by 32-bit buffer offsets
+  if ((long)rows * HD * 2 >= (1L << 31) || (long)HD * rp * 2 >= (1L << 31) || rp < rows)
+    return hipErrorInvalidValue;
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // 64^-0.5 * log2(e)
   hipLaunchKernelGGL(attention_kernel, dim3(n_tiles * heads), dim3(256), 0, stream, q, k, vt, o,
                      doc_start, doc_len, tiles, rows, rp, heads, chunk, scale_log2);
