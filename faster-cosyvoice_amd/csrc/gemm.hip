@@ -5,14 +5,16 @@
 // the bf16 peak in a register loop, the 16x16x32 form ~54%).
 //
 // Main loop.  A workgroup of WM x WN waves owns a BM x BN tile (256x256, 192x256, 128x256 and
-// 256x128 with 8 waves, 128x128 and 32x128 with 4 waves, several workgroups per CU); each wave
-// a sub-tile of 32x32 MFMA tiles.  Operands go straight from global memory into LDS with
-// global_load_lds_dwordx4 (no register staging, no ds_write) through a ring of slices (by
-// default two stages of K = 64: one wave-level copy fills 1 KB of LDS = 8 rows x 128 B, so every
-// L2 request is a full 128-byte line).  The 16-byte chunks of a row sit at a row-rotated position, so 16 consecutive rows read
-// at one chunk index hit 16 distinct 16-byte bank groups.  Inside a slice the fragments of
-// k-step ks+1 are read while the MFMAs of k-step ks run.  The tile shape is chosen per call to
-// balance the last round of tiles over the 256 CUs.
+// 256x128 with 8 waves, 160x256, 128x128 and 32x128 with 4 waves, several workgroups per CU);
+// each wave a sub-tile of 32x32 MFMA tiles.  Operands go straight from global memory into LDS
+// with global_load_lds_dwordx4 (no register staging, no ds_write; scalar base and LDS address,
+// per-lane 32-bit offset) through a ring of slices (by default two stages of K = 64: one
+// wave-level copy fills 1 KB of LDS = 8 rows x 128 B, so every L2 request is a full 128-byte
+// line).  The 16-byte chunks of a row sit at a row-rotated position, so 16 consecutive rows
+// read at one chunk index hit 16 distinct 16-byte bank groups.  Inside a slice the fragments of
+// k-step ks+1 are read while the MFMAs of k-step ks run, and the loop is rotated so that a
+// slice's last k-step runs after the barrier that publishes the next slice.  The tile shape is
+// chosen per call from the tile rounds over the 256 CUs and per-shape rates.
 
 // Operand roles are swapped: the MFMA computes D = W_tile . A_tile^T, so the accumulator of a
 // 32x32 tile holds, in lane l, output row m = l % 32 and four consecutive output columns per
