@@ -114,6 +114,19 @@ def test_plan_rejects_bad_layouts(fcv, handle, cu, match):
         _lib.check(_plan(_lib, handle, cu))
 
 
+def test_plan_rejects_layouts_past_32bit_offsets(fcv, handle):
+    """256 documents of 4096 rows: (rows + 7 per document) x 4 KB of residual row reaches 4 GB,
+    past what the kernels' 32-bit byte offsets address."""
+    from faster_cosyvoice_amd import _lib
+    cu = [4096 * i for i in range(257)]
+    with pytest.raises(ValueError, match="too many rows"):
+        _lib.check(_plan(_lib, handle, cu))
+    # one document fewer fits the offsets and fails the next check, the workspace size, before
+    # anything touches a device
+    with pytest.raises(ValueError, match="too small"):
+        _lib.check(_plan(_lib, handle, cu[:-1], nbytes=1024))
+
+
 def test_plan_rejects_bad_mask_and_workspace(fcv, handle):
     from faster_cosyvoice_amd import _lib
     with pytest.raises(ValueError, match="mask_mode"):
