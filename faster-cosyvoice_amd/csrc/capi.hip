@@ -348,12 +348,13 @@ int fcv_dit_plan(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask
                   std::to_string(m->dims.max_pos));
   }
   const int rows = cu_host[n_docs];
-  // the kernels address activations by 32-bit byte offsets: the widest row (the FF hidden row
-  // in bf16 or the fp32 residual row) times the internal rows must stay below 4 GB
+  // the kernels address activations by 32-bit byte offsets within buffer ranges held as an
+  // int: the widest row (the FF hidden row in bf16 or the fp32 residual row) times the internal
+  // rows must stay below 2 GB
   const long row_bytes = std::max<long>(2L * m->dims.ff_dim, 4L * m->dims.dim);
-  FCV_CHECK(internal_rows_bound(rows, n_docs) * row_bytes < (1L << 32), FCV_ERR_INVALID,
+  FCV_CHECK(internal_rows_bound(rows, n_docs) * row_bytes < (1L << 31), FCV_ERR_INVALID,
             "too many rows: (rows + 7 per document) x " + std::to_string(row_bytes) +
-                " bytes must stay below 4 GB");
+                " bytes must stay below 2 GB");
 
   // internal layout: document starts rounded up to multiples of 8 rows
   std::vector<int32_t> cu_int(n_docs + 1, 0), lens(n_docs);

@@ -368,7 +368,7 @@ struct BiasCol { float4 b; };
 
 // Raw buffer accesses (stride 0) over [base, base + bytes): a load past `bytes` reads zeros and a
 // store past it is dropped, so row guards (row >= M) cost no branch, and the offsets are 32-bit
-// (the callers' M x ld x element size stays below 4 GB).
+// (the callers check that M x ld x element size stays below 2 GB, the range being an int).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
@@ -695,14 +695,14 @@ hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, c
 
 hipError_t gemm_bias_gelu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, bf16* out, int ldo, hipStream_t stream) {
-  if ((long)M * ldo * 2 >= (1L << 32)) return hipErrorInvalidValue;  // 32-bit buffer offsets
+  if ((long)M * ldo * 2 >= (1L << 31)) return hipErrorInvalidValue;  // buffer range is an int
   return launch(A, lda, W, ldw, M, N, K, EpiBiasGeluBf16{bias, out, ldo}, stream);
 }
 
 hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, float* h, int ldh, const float* gate,
                                long mod_stride, const int32_t* docid, hipStream_t stream) {
-  if ((long)M * ldh * 4 >= (1L << 32)) return hipErrorInvalidValue;  // 32-bit buffer offsets
+  if ((long)M * ldh * 4 >= (1L << 31)) return hipErrorInvalidValue;  // buffer range is an int
   if (mod_stride == 0)
     return launch(A, lda, W, ldw, M, N, K,
                   EpiGatedResidual<false>{bias, h, ldh, gate, 0, docid}, stream);

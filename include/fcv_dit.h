@@ -85,8 +85,8 @@ size_t fcv_dit_workspace_bytes(const FcvDit* dit, int32_t rows, int32_t n_docs);
  * flashinfer_attention.py:88-123, and _get_packed_layout, flashinfer_dit.py:364-405).
  * cu_seqlens_host: [n_docs+1] exclusive prefix sums, cu[0] = 0, non-decreasing, every
  * document 1 <= length <= max_pos, and (rows + 7 per document) x max(2 ff_dim, 4 dim) bytes
- * below 4 GB (the kernels address activations by 32-bit byte offsets; about 10^6 rows at the
- * Token2Wav dims).  mask_mode: FCV_MASK_FULL or FCV_MASK_CHUNK_CAUSAL
+ * below 2 GB (the kernels address activations by 32-bit byte offsets; about 5 x 10^5 rows at
+ * the Token2Wav dims).  mask_mode: FCV_MASK_FULL or FCV_MASK_CHUNK_CAUSAL
  * (key k visible to query q iff k/chunk <= q/chunk, flashinfer_attention.py:16-33).
  * The workspace is bound to the handle until the next plan.  Synchronous on `stream`. */
 int fcv_dit_plan(FcvDit* dit, const int32_t* cu_seqlens_host, int32_t n_docs, int32_t mask_mode,

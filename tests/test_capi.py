@@ -115,10 +115,10 @@ def test_plan_rejects_bad_layouts(fcv, handle, cu, match):
 
 
 def test_plan_rejects_layouts_past_32bit_offsets(fcv, handle):
-    """256 documents of 4096 rows: (rows + 7 per document) x 4 KB of residual row reaches 4 GB,
-    past what the kernels' 32-bit byte offsets address."""
+    """128 documents of 4096 rows: (rows + 7 per document) x 4 KB of residual row passes 2 GB,
+    past what the kernels' 32-bit buffer ranges address."""
     from faster_cosyvoice_amd import _lib
-    cu = [4096 * i for i in range(257)]
+    cu = [4096 * i for i in range(129)]
     with pytest.raises(ValueError, match="too many rows"):
         _lib.check(_plan(_lib, handle, cu))
     # one document fewer fits the offsets and fails the next check, the workspace size, before
