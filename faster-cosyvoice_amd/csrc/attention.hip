@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
   // multiple of 8 (documents start 8-aligned); keys at or past kv_end are zeroed when the chunk
   // is stashed.  The next tile is fetched unconditionally (the surplus tile lands in the buffer
   // no later iteration reads), so the compiler never waits on a load before the stash that
-  // consumes it.
+  // consumes it.  (Descriptor word 3 = 0x00020000: 32-bit data format, no swizzle.)
   const int lr = tid >> 3;         // 0..31
   const int lc = (tid & 7) * 8;    // 0..56
   const __amdgpu_buffer_rsrc_t k_rsrc =

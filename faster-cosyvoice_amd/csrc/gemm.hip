@@ -369,6 +369,8 @@ struct BiasCol { float4 b; };
 // Raw buffer accesses (stride 0) over [base, base + bytes): a load past `bytes` reads zeros and a
 // store past it is dropped, so row guards (row >= M) cost no branch, and the offsets are 32-bit
 // (the callers check that M x ld x element size stays below 2 GB, the range being an int).
+// Descriptor word 3 = 0x00020000: DATA_FORMAT 32 bits (bits 15-18 = 4), no swizzle, the
+// setting raw (untyped) buffer accesses use on this GPU family.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
