@@ -1,16 +1,18 @@
-// Skinny products out[m, n] = f(sum_k W[n, k] a[m, k] + bias[n]) for M <= 4 rows of a: the
+// Skinny products out[m, n] = f(sum_k W[n, k] a[m, k] + bias[n]) for M <= 16 rows of a: the
 // timestep MLP and the AdaLN projection, whose time is reading W (the concatenated AdaLN
 // weights are 137216 x 1024 bf16 = 281 MB per evaluation).  Bandwidth-bound, so no MFMA: one
 // wave owns 4 rows of W; lane l reads k in [8l, 8l + 8) of every 512-wide k block, so each load
-// instruction covers 1 KB of one W row contiguously; the wave's 4 x M partial sums are reduced
-// with cross-lane shuffles and written by lane 0.
+// instruction covers 1 KB of one W row contiguously.  The rows of a are taken in chunks of up
+// to 4 against the W rows held in registers; each chunk's 4 x 4 partial sums are reduced with
+// cross-lane shuffles and written by lane 0.  Every output element is summed in the same order
+// whatever M is, so a row's result does not depend on how many rows share the launch.
 #include "kernels.hpp"
 
 namespace fcv {
 namespace {
 
 constexpr int kGemvRows = 4;   // W rows per wave
-constexpr int kGemvMaxM = 4;
+constexpr int kGemvMaxM = 16;  // rows of a per launch (in chunks of up to 4)
 
 struct GemvF32 {
   const float* bias;
@@ -28,7 +30,8 @@ struct GemvSiluBf16 {
   }
 };
 
-// K % 512 == 0: lane l holds k = 512 b + 8 l + 0..7 for each of the K / 512 blocks b
+// K % 512 == 0: lane l holds k = 512 b + 8 l + 0..7 for each of the K / 512 blocks b.  MM rows
+// of a per chunk; ceil(M / MM) chunks.
 template <int K, int MM, class Epi>
 __global__ __launch_bounds__(256) void gemv_kernel(const bf16* __restrict__ a, int lda,
                                                    const bf16* __restrict__ W, int ldw, int M,
@@ -37,16 +40,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(const bf16* __restrict__ a, i
   const int lane = threadIdx.x & 63;
   const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kGemvRows;
   if (n0 >= N) return;
-  float av[MM][KB][8];
-#pragma unroll
-  for (int m = 0; m < MM; ++m)
-#pragma unroll
-    for (int b = 0; b < KB; ++b) {
-      const bf16x8 v = m < M ? *reinterpret_cast<const bf16x8*>(a + (long)m * lda + 512 * b + 8 * lane)
-                             : bf16x8{};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) av[m][b][e] = bf2f(v[e]);
-    }
   bf16x8 wv[kGemvRows][KB];
 #pragma unroll
   for (int r = 0; r < kGemvRows; ++r)
@@ -54,24 +47,38 @@ __global__ __launch_bounds__(256) void gemv_kernel(const bf16* __restrict__ a, i
     for (int b = 0; b < KB; ++b)
       wv[r][b] = *reinterpret_cast<const bf16x8*>(W + (long)min(n0 + r, N - 1) * ldw + 512 * b +
                                                   8 * lane);
-  float acc[kGemvRows][MM];
-#pragma unroll
-  for (int r = 0; r < kGemvRows; ++r)
-#pragma unroll
-    for (int m = 0; m < MM; ++m) {
-      float s = 0.0f;
-#pragma unroll
-      for (int b = 0; b < KB; ++b)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s = fmaf(bf2f(wv[r][b][e]), av[m][b][e], s);
-      acc[r][m] = wave_sum(s);
-    }
-  if (lane != 0) return;
-#pragma unroll
-  for (int r = 0; r < kGemvRows; ++r)
+  for (int m0 = 0; m0 < M; m0 += MM) {
+    float av[MM][KB][8];
 #pragma unroll
     for (int m = 0; m < MM; ++m)
-      if (m < M && n0 + r < N) epi(m, n0 + r, acc[r][m]);
+#pragma unroll
+      for (int b = 0; b < KB; ++b) {
+        const bf16x8 v = m0 + m < M
+                             ? *reinterpret_cast<const bf16x8*>(a + (long)(m0 + m) * lda + 512 * b + 8 * lane)
+                             : bf16x8{};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) av[m][b][e] = bf2f(v[e]);
+      }
+    float acc[kGemvRows][MM];
+#pragma unroll
+    for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+      for (int m = 0; m < MM; ++m) {
+        float s = 0.0f;
+#pragma unroll
+        for (int b = 0; b < KB; ++b)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s = fmaf(bf2f(wv[r][b][e]), av[m][b][e], s);
+        acc[r][m] = wave_sum(s);
+      }
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+          if (m0 + m < M && n0 + r < N) epi(m0 + m, n0 + r, acc[r][m]);
+    }
+  }
 }
 
 template <int K, class Epi>
@@ -85,8 +92,8 @@ hipError_t launch_gemv_k(const bf16* a, int lda, const bf16* W, int ldw, int M, 
     hipLaunchKernelGGL((gemv_kernel<K, 2, Epi>), dim3(blocks), dim3(256), 0, stream, a, lda, W,
                        ldw, M, N, epi);
   else
-    hipLaunchKernelGGL((gemv_kernel<K, kGemvMaxM, Epi>), dim3(blocks), dim3(256), 0, stream, a,
-                       lda, W, ldw, M, N, epi);
+    hipLaunchKernelGGL((gemv_kernel<K, 4, Epi>), dim3(blocks), dim3(256), 0, stream, a, lda, W,
+                       ldw, M, N, epi);
   return hipGetLastError();
 }
 
