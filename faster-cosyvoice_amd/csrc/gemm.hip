@@ -674,7 +674,9 @@ hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const f
                          int M, int N, int K, float* out, int ldo, int n_valid,
                          hipStream_t stream) {
   if (n_valid % 4 != 0) return hipErrorInvalidValue;
-  // a few rows (the AdaLN projection of a shared t): reading W is all the work
+  // the AdaLN projection and the time MLP (one row per distinct t): reading W is all the work,
+  // and the skinny product sums a row the same way whatever the row count, so a document's
+  // modulation does not depend on how many t rows the call carries
   if (n_valid == N && gemv_supported(M, K, lda, ldw))
     return gemv_bias_f32(A, lda, W, ldw, bias, M, N, K, out, ldo, stream);
   return launch(A, lda, W, ldw, M, N, K, EpiBiasF32{bias, out, ldo, n_valid}, stream);

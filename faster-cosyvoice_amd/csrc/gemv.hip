@@ -1,11 +1,13 @@
-// Skinny products out[m, n] = f(sum_k W[n, k] a[m, k] + bias[n]) for M <= 16 rows of a: the
-// timestep MLP and the AdaLN projection, whose time is reading W (the concatenated AdaLN
-// weights are 137216 x 1024 bf16 = 281 MB per evaluation).  Bandwidth-bound, so no MFMA: one
-// wave owns 4 rows of W; lane l reads k in [8l, 8l + 8) of every 512-wide k block, so each load
-// instruction covers 1 KB of one W row contiguously.  The rows of a are taken in chunks of up
-// to 4 against the W rows held in registers; each chunk's 4 x 4 partial sums are reduced with
-// cross-lane shuffles and written by lane 0.  Every output element is summed in the same order
-// whatever M is, so a row's result does not depend on how many rows share the launch.
+// Skinny products out[m, n] = f(sum_k W[n, k] a[m, k] + bias[n]) for rows of a that share
+// one W: the timestep MLP and the AdaLN projection, whose time is reading W (the concatenated
+// AdaLN weights are 137216 x 1024 bf16 = 281 MB per evaluation).  Bandwidth-bound, so no MFMA:
+// one wave owns 4 rows of W; lane l reads k in [8l, 8l + 8) of every 512-wide k block, so each
+// load instruction covers 1 KB of one W row contiguously.  A launch takes up to 16 rows of a,
+// in chunks of up to 4 against the W rows held in registers; each chunk's 4 x 4 partial sums
+// are reduced with cross-lane shuffles and written by lane 0.  More rows take more launches of
+// 16.  Every output element is summed in the same order whatever M is, so a row's result does
+// not depend on how many rows share the call (one shared t, one t per document, or the t
+// values of a solver's steps all give a t the same modulation row, bit for bit).
 #include "kernels.hpp"
 
 namespace fcv {
@@ -108,19 +110,29 @@ hipError_t launch_gemv(const bf16* a, int lda, const bf16* W, int ldw, int M, in
 }  // namespace
 
 bool gemv_supported(int M, int K, int lda, int ldw) {
-  return M >= 1 && M <= kGemvMaxM && (K == 1024 || K == 512) && lda % 8 == 0 && ldw % 8 == 0;
+  return M >= 1 && (K == 1024 || K == 512) && lda % 8 == 0 && ldw % 8 == 0;
 }
 
 hipError_t gemv_bias_f32(const bf16* a, int lda, const bf16* W, int ldw, const float* bias, int M,
                          int N, int K, float* out, int ldo, hipStream_t stream) {
   if (!gemv_supported(M, K, lda, ldw)) return hipErrorInvalidValue;
-  return launch_gemv(a, lda, W, ldw, M, N, K, GemvF32{bias, out, ldo}, stream);
+  for (int m0 = 0; m0 < M; m0 += kGemvMaxM) {
+    const hipError_t e = launch_gemv(a + (long)m0 * lda, lda, W, ldw, min(kGemvMaxM, M - m0), N, K,
+                                     GemvF32{bias, out + (long)m0 * ldo, ldo}, stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t gemv_bias_silu_bf16(const bf16* a, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, bf16* out, int ldo, hipStream_t stream) {
   if (!gemv_supported(M, K, lda, ldw)) return hipErrorInvalidValue;
-  return launch_gemv(a, lda, W, ldw, M, N, K, GemvSiluBf16{bias, out, ldo}, stream);
+  for (int m0 = 0; m0 < M; m0 += kGemvMaxM) {
+    const hipError_t e = launch_gemv(a + (long)m0 * lda, lda, W, ldw, min(kGemvMaxM, M - m0), N, K,
+                                     GemvSiluBf16{bias, out + (long)m0 * ldo, ldo}, stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace fcv

@@ -254,7 +254,11 @@ __global__ __launch_bounds__(64) void f0_head_kernel(const double* __restrict__ 
 // One thread per (document, harmonic): the per-frame phase increment of harmonic h is
 // rad = frac(f0 (h+1) / sr); the frame-rate value is the linear interpolation the reference
 // takes from the sample-rate sequence (whose first sample also carries rand_ini[h]); the
-// phase is the running sum in frame order, times 2 pi, times the upsampling scale.
+// phase is the running sum in frame order, times 2 pi, times the upsampling scale.  The running
+// sum is held in fp64 and rounded to fp32 at every frame, which is what the reference's
+// torch.cumsum over the fp32 rad values (cosyvoice/hifigan/generator.py:255) computes on the
+// CPU, whose kernel accumulates fp32 in double: an fp32 running sum drifts by ~1e-6 relative
+// per few hundred frames, and the phase multiplies that by 2 pi x 480.
 __global__ __launch_bounds__(64) void source_phase_kernel(const HiftSource p,
                                                           const HiftDocs docs) {
 #pragma clang fp contract(off)
@@ -273,7 +277,7 @@ __global__ __launch_bounds__(64) void source_phase_kernel(const HiftSource p,
     if (i == 0) v = v + p.rand_ini[h];
     return v;
   };
-  float c = 0.0f;
+  double c = 0.0;
   for (int t = 0; t < T; ++t) {
     float src = scale * ((float)t + 0.5f) - 0.5f;
     if (src < 0.0f) src = 0.0f;
@@ -283,8 +287,8 @@ __global__ __launch_bounds__(64) void source_phase_kernel(const HiftSource p,
     const long i1 = i0 + (i0 < L - 1 ? 1 : 0);
     const float a = l0 * rad_at(i0);
     const float b = l1 * rad_at(i1);
-    c = c + (a + b);
-    float ph = (c * 2.0f) * 3.14159265358979323846f;
+    c = c + (double)(a + b);
+    float ph = ((float)c * 2.0f) * 3.14159265358979323846f;
     ph = ph * scale;
     p.sines[(long)(f_base + t) * p.H + h] = sinf(ph) * p.sine_amp;
   }

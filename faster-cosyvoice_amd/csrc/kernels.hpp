@@ -48,7 +48,8 @@ hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const f
                          const float* rope_sin, int rope_dim, int max_pos, bf16* q, bf16* k,
                          bf16* vt, int rp, hipStream_t stream);
 
-// ---- skinny products (M <= 4 rows, K in {512, 1024}): bandwidth-bound, no MFMA -----------
+// ---- skinny products (few rows sharing W, K in {512, 1024}): bandwidth-bound, no MFMA -------
+// Launches of up to 16 rows each; a row's result is the same whatever M is.
 bool gemv_supported(int M, int K, int lda, int ldw);
 // out[m, n] = acc + bias[n]
 hipError_t gemv_bias_f32(const bf16* a, int lda, const bf16* W, int ldw, const float* bias, int M,

@@ -381,9 +381,11 @@ class DiTEstimator(nn.Module, _PackedRunner):
             _lib.check(lib.fcv_pack_padded(handle, f32(src).data_ptr(), batch, mel, padded,
                                            dst.data_ptr(), stream))
             packed[name] = dst
-        t = f32(t)
-        if t.ndim == 0 or t.numel() == 1:
-            t = t.reshape(1)
+        t = f32(t).reshape(-1)
+        # the packed solver hands every document the same t (flashinfer_flow.py:53-57): one
+        # modulation row then serves all of them (bit-identical to one row per document)
+        if t.numel() > 1 and bool((t == t[0]).all()):
+            t = t[:1]
         spk = f32(spks).reshape(batch, mel)
         v = torch.empty(rows, mel, dtype=torch.float32, device=dev)
         _lib.check(lib.fcv_dit_forward(handle, packed["x"].data_ptr(), packed["mu"].data_ptr(),

@@ -88,18 +88,27 @@ def state_dict_shapes(d: DiTDims) -> list[tuple[str, tuple[int, ...]]]:
 
 
 def random_state_dict(dims: DiTDims = DiTDims(), seed: int = 0, std: float = 0.02,
-                      gate_bias: float = 0.0) -> dict[str, torch.Tensor]:
+                      gate_bias: float = 0.0, qk_std: float | None = None
+                      ) -> dict[str, torch.Tensor]:
     """Every parameter ~ N(0, std), drawn in registration order from one PCG64 stream.
 
     ``gate_bias`` (>0) adds a constant to the AdaLN gate biases (chunks 2 and 5
     of each block's 6-way modulation) so that every block changes the
     residual stream by O(gate_bias); the default keeps plain N(0, 0.02),
     where the gates are small but nonzero.
+
+    ``qk_std`` (when given) draws the ``to_q`` / ``to_k`` weights with that deviation instead
+    (the same draws, rescaled).  With unit-variance normalised inputs the attention logits
+    q.k/8 then have a deviation of about ``1024 qk_std^2`` (0.4 at 0.02, 3.7 at 0.06), so the
+    softmax is peaked and the output depends on which keys are visible and on RoPE.
     """
     rng = np.random.Generator(np.random.PCG64(seed))
     sd = {}
     for name, shape in state_dict_shapes(dims):
-        arr = rng.standard_normal(int(np.prod(shape)), dtype=np.float32) * np.float32(std)
+        sigma = std
+        if qk_std is not None and (name.endswith("to_q.weight") or name.endswith("to_k.weight")):
+            sigma = qk_std
+        arr = rng.standard_normal(int(np.prod(shape)), dtype=np.float32) * np.float32(sigma)
         sd[name] = torch.from_numpy(arr.reshape(shape))
     if gate_bias:
         for i in range(dims.depth):

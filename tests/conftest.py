@@ -46,3 +46,16 @@ def full22(fcv):
     say("[full22] drawing 22-layer weights")
     sd = fcv.synthetic.random_state_dict(fcv.synthetic.DiTDims(), seed=0)
     return sd, make_estimator(fcv, sd, depth=22)
+
+
+@pytest.fixture(scope="session")
+def sharp22(fcv):
+    """The 22-block DiT on the peaked-attention recipe of ``tests/recipes.py`` (GPU tests only)."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from tests import recipes
+    from tests.gpu_helpers import make_estimator, say
+    say("[sharp22] drawing 22-layer weights, peaked-attention recipe")
+    sd = recipes.state_dict(fcv, recipes.SHARP22)
+    return sd, make_estimator(fcv, sd, depth=22)

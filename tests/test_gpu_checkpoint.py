@@ -1,12 +1,16 @@
-"""GPU check of ``load_flow``: a flow built from a saved ``flow.pt`` gives bit-identical Mel to
-one assembled by hand from the same tensors (the loader only routes weights)."""
+"""GPU checks of ``load_flow``: a flow built from a saved ``flow.pt`` gives bit-identical Mel to
+one assembled by hand from the same tensors (the loader only routes weights), and the same Mel
+as the oracle pipeline (front-end oracle + 10-step CFG Euler solve over the DiT oracle) run on
+the state dict that was saved, within rel-L2 2e-2."""
 
 from __future__ import annotations
 
 import pytest
 import torch
 
-from tests.gpu_helpers import make_estimator, say
+from oracle import dit_oracle as O
+from oracle import frontend_oracle as F
+from tests.gpu_helpers import make_estimator, rel_l2, say
 
 pytestmark = pytest.mark.gpu
 
@@ -40,6 +44,24 @@ def test_load_flow_matches_hand_assembled_flow(fcv, tmp_path):
     a = fcv.flow_inference_batched(loaded, toks, prompts, xvec, noise=noise)
     b = fcv.flow_inference_batched(fe, toks, prompts, xvec, noise=noise)
     assert all(torch.equal(x, y) for x, y in zip(a, b))
+
+    say("[ckpt] oracle pipeline on the saved state dict")
+    mu, cond, spks, mel, plens = F.flow_inputs(front, toks, prompts, xvec.cpu())
+    mask = torch.zeros(2, 1, max(mel))
+    for i, m in enumerate(mel):
+        mask[i, 0, :m] = 1
+
+    def oracle_est(x, mask, mu, t, spks, cond, streaming):
+        return O.dit_forward(dit, x, mask, mu, t, spks, cond, streaming=streaming)
+
+    ref = O.solve_euler_batched(oracle_est, noise.cpu(), mu, mask, spks, cond, n_steps=10,
+                                cfg_rate=0.7)
+    for i in range(2):
+        want = ref[i:i + 1, :, plens[i]:mel[i]]
+        assert a[i].shape == want.shape
+        err = rel_l2(a[i].cpu(), want)
+        say(f"[ckpt] request {i}: Mel rel_l2 vs oracle pipeline {err:.2e}")
+        assert err <= 2e-2
     sa = fcv.flow_inference_batched_streaming(loaded, toks, prompts, xvec, [False, True])
     sb = fcv.flow_inference_batched_streaming(fe, toks, prompts, xvec, [False, True])
     assert all(torch.equal(x, y) for x, y in zip(sa, sb))

@@ -50,6 +50,35 @@ def test_vocoder_matches_oracle(hift, finalize):
     assert ew <= 1e-4
 
 
+def test_long_requests_packed_match_oracle(fcv):
+    """Three requests of 600-700 frames (12-14 s of audio each) in one packed call against the
+    oracle run on each alone: the harmonic source phase reaches ~1e6 rad over such a request and
+    is accumulated sequentially in the reference's fp32 order, so the source stays within 1e-5
+    absolute and the waveform within rel-L2 1e-4 over the whole length."""
+    dims = fcv.synthetic.HiFTDims()
+    sd = fcv.synthetic.random_hift_state_dict(dims, seed=75)
+    frames = (640, 700, 613)
+    buf = fcv.synthetic.random_hift_buffers(dims, max_samples=480 * max(frames), seed=76)
+    v = fcv.HiFTVocoder(dims, device="cuda:0", buffers=buf)
+    v.load_reference_state_dict(sd)
+    v.finalize_weights()
+    folded = H.fold_weight_norm(sd)
+    g = torch.Generator().manual_seed(77)
+    mels = [torch.randn(80, n, generator=g) for n in frames]
+    fin = [True, False, True]
+    say(f"[hift long] packed call, {sum(frames)} frames")
+    speech, source = v.inference_batched([m.cuda() for m in mels], fin, return_source=True)
+    for i, (m, f) in enumerate(zip(mels, fin)):
+        say(f"[hift long] oracle, request {i} ({m.shape[1]} frames, finalize={f})")
+        ref, ref_s = H.inference(folded, m[None], buf, dims, f)
+        assert speech[i].shape == ref.shape and source[i].shape == ref_s.shape
+        es = float((source[i].cpu() - ref_s).abs().max())
+        ew = rel_l2(speech[i].cpu(), ref)
+        say(f"[hift long] request {i}: source max abs {es:.2e}, waveform rel_l2 {ew:.2e}")
+        assert es <= 1e-5
+        assert ew <= 1e-4
+
+
 def test_packed_requests_equal_requests_alone(hift):
     """Three requests of different lengths, final and not: one packed call or one call each
     gives bit-identical waveforms."""

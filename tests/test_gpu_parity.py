@@ -15,6 +15,7 @@ import pytest
 import torch
 
 from oracle import dit_oracle as O
+from tests import recipes
 from tests.gpu_helpers import (bf16_weights, make_estimator, oracle_packed, random_packed, rel_l2,
                                say)
 
@@ -152,21 +153,115 @@ def test_concurrent_request_groups_equal_one_batch(fcv, stress2):
 
 
 def test_shared_t_equals_per_doc_t(fcv, stress2):
-    """One shared t vs the same t per document.  Up to 4 t rows the time MLP and the AdaLN
-    projection take the same bandwidth-bound path either way (bitwise equal); with more rows
-    they run on the MFMA GEMM, whose fp32 summation order differs, and the bf16 rounding of the
-    time embedding then flips in a few places, so the outputs agree to about 1e-3."""
+    """One shared t against the same t repeated per document, for 2, 16 and 20 documents.  The
+    time MLP's second layer and the AdaLN projection run on the skinny product, which sums
+    every row the same way whatever the row count (launches of up to 16 rows), so the
+    velocities are bit-identical.  With 20 distinct t values (two launches) every document's
+    rows equal that document run alone at its own t, so the rows past the first launch are
+    indexed right."""
     sd, est = stress2
-    lengths = [50, 70]
-    x, mu, cond, spks, _ = random_packed(lengths, seed=3)
-    a = est.forward_packed(x, mu, cond, spks, torch.tensor([0.3]), lengths)
-    b = est.forward_packed(x, mu, cond, spks, torch.tensor([0.3, 0.3]), lengths)
-    assert torch.equal(a, b)
-    lengths = [50, 70, 9, 33, 64, 20]
-    x, mu, cond, spks, _ = random_packed(lengths, seed=3)
-    a = est.forward_packed(x, mu, cond, spks, torch.tensor([0.3]), lengths).cpu()
-    b = est.forward_packed(x, mu, cond, spks, torch.full((6,), 0.3), lengths).cpu()
-    assert rel_l2(a, b) < 5e-3
+    g = torch.Generator().manual_seed(3)
+    for n_docs in (2, 16, 20):
+        lengths = torch.randint(1, 80, (n_docs,), generator=g).tolist()
+        x, mu, cond, spks, _ = random_packed(lengths, seed=n_docs)
+        say(f"[shared_t] {n_docs} documents")
+        a = est.forward_packed(x, mu, cond, spks, torch.tensor([0.3]), lengths)
+        b = est.forward_packed(x, mu, cond, spks, torch.full((n_docs,), 0.3), lengths)
+        assert torch.equal(a, b), n_docs
+    t = torch.rand(n_docs, generator=g)
+    full = est.forward_packed(x, mu, cond, spks, t, lengths)
+    off = 0
+    for d, n in enumerate(lengths):
+        alone = est.forward_packed(x[off:off + n], mu[off:off + n], cond[off:off + n],
+                                   spks[d:d + 1], t[d:d + 1], [n])
+        assert torch.equal(alone, full[off:off + n]), d
+        off += n
+
+
+def test_padded_dropin_collapses_equal_t(fcv, stress2):
+    """The padded drop-in gets t of length 2B, all equal, from the packed solver
+    (flashinfer_flow.py:53-57); it computes one modulation row and gives the rows of the
+    packed call with a shared t, bit for bit, for 2B = 24 documents."""
+    sd, est = stress2
+    g = torch.Generator().manual_seed(9)
+    lengths = torch.randint(8, 60, (24,), generator=g).tolist()
+    T = max(lengths)
+    x, mu, cond, spks, _ = random_packed(lengths, seed=10)
+    pad = lambda rows: O.unpack(rows, lengths, T)
+    mask = torch.zeros(24, 1, T)
+    for b, n in enumerate(lengths):
+        mask[b, 0, :n] = 1
+    dev = "cuda:0"
+    out = est(pad(x).to(dev), mask.to(dev), pad(mu).to(dev), torch.full((24,), 0.55, device=dev),
+              spks.to(dev), pad(cond).to(dev)).cpu()
+    packed = est.forward_packed(x, mu, cond, spks, torch.tensor([0.55]), lengths).cpu()
+    assert torch.equal(O.pack(out, lengths), packed)
+
+
+def test_solve_twenty_steps_equals_stepwise(fcv, stress2):
+    """A 20-step solve computes the modulation rows of steps 0-15 in one pass and of steps
+    16-19 in a second one.  Eager, on its first capture and on a replay, it gives bit for bit
+    the sample of 20 single forwards (each with its own shared t) each followed by the CFG
+    Euler update of the C ABI, with the same cosine schedule."""
+    _, est = stress2
+    b = fcv.synthetic.make_batch("steps20", [70, 33, 41], [20, 10, 15], seed=61)
+    ts, dts = fcv.euler_schedule(20)
+    rc = sum(b.lengths)
+    inp = b.cfg_inputs()
+    dev = "cuda:0"
+    x = inp["x"].to(dev)
+    lib = fcv._lib.load()
+    say("[steps20] stepwise forwards")
+    for i in range(20):
+        v = est.forward_packed(x, inp["mu"], inp["cond"], inp["spks"], torch.tensor([ts[i]]),
+                               b.doc_lengths)
+        fcv._lib.check(lib.fcv_euler_cfg_step(est._require(), x.data_ptr(), v.data_ptr(), dts[i],
+                                              0.7, est._stream_ptr()))
+    want = x[:rc].cpu()
+    for graph in (False, True, True):
+        say(f"[steps20] solve use_graph={graph}")
+        got = fcv.solve_euler_packed(est, b.noise, b.mu, b.cond, b.spks, b.lengths, n_steps=20,
+                                     use_graph=graph, concurrency=1).cpu()
+        assert torch.equal(got, want), graph
+
+
+@pytest.mark.parametrize("streaming", [False, True])
+def test_peaked_attention_depth22(fcv, sharp22, streaming):
+    """22 blocks on the peaked-attention recipe (q/k weights of deviation 0.05, gates +0.2):
+    the 550-frame CFG pair against the fp32 oracle.  On these weights and inputs dropping or
+    reversing RoPE, a uniform softmax or a chunk boundary one frame off moves the oracle
+    velocity by 5-50x the tolerance (tests/test_oracle_power.py), so this bar pins the RoPE
+    epilogue, the softmax and the chunk-causal mask."""
+    sd, est = sharp22
+    x, mu, cond, spks, t, lengths = recipes.cfg_pair_inputs(fcv)
+    say(f"[peaked22] streaming={streaming} GPU forward")
+    v = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming).cpu()
+    say(f"[peaked22] streaming={streaming} oracle forward")
+    ref = oracle_packed(sd, x, mu, cond, spks, t, lengths, streaming)
+    err = rel_l2(v, ref)
+    say(f"[peaked22] streaming={streaming} velocity rel_l2 vs fp32 oracle {err:.2e}")
+    assert err <= recipes.VEL_TOL
+
+
+@pytest.mark.parametrize("streaming", [False, True])
+def test_peaked_attention_max_pos_document(fcv, streaming):
+    """A document as long as the RoPE tables (4096 rows) between 24 short ones, 2 blocks on the
+    peaked-attention recipe, against the fp32 oracle: the long document on its own (RoPE up to
+    the tables' last row; dropping, reversing or freezing RoPE past row 2048 moves it by
+    5-8x the tolerance) and the short documents together."""
+    sd = recipes.state_dict(fcv, recipes.SHARP2)
+    est = make_estimator(fcv, sd, depth=2, max_pos=recipes.MAX_POS)
+    x, mu, cond, spks, t, lengths = recipes.max_pos_inputs()
+    say(f"[peaked_max_pos] streaming={streaming} {len(lengths)} docs, GPU forward")
+    v = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming).cpu()
+    say(f"[peaked_max_pos] streaming={streaming} oracle forward")
+    ref = oracle_packed(sd, x, mu, cond, spks, t, lengths, streaming)
+    long = recipes.long_doc_rows(lengths)
+    rest = torch.ones(v.shape[0], dtype=torch.bool)
+    rest[long] = False
+    e_long, e_rest = rel_l2(v[long], ref[long]), rel_l2(v[rest], ref[rest])
+    say(f"[peaked_max_pos] streaming={streaming} rel_l2 long {e_long:.2e} short docs {e_rest:.2e}")
+    assert e_long <= recipes.VEL_TOL and e_rest <= recipes.VEL_TOL
 
 
 def test_padded_dropin_matches_packed(fcv, stress2):
