@@ -93,6 +93,9 @@ SIGNATURES = {
     "fcv_flow_token_features": (c_int32, [POINTER(FcvFlowDims), POINTER(FcvFlowWeights), c_void_p,
                                           POINTER(c_int32), POINTER(c_int32), c_int32, c_void_p,
                                           c_void_p, c_size_t, c_void_p]),
+    "fcv_flow_token_features_noalloc": (c_int32, [POINTER(FcvFlowDims), POINTER(FcvFlowWeights),
+                                                  c_void_p, POINTER(c_int32), POINTER(c_int32),
+                                                  c_int32, c_void_p, c_void_p]),
     "fcv_flow_speaker": (c_int32, [POINTER(FcvFlowDims), POINTER(FcvFlowWeights), c_void_p,
                                    c_int32, c_void_p, c_void_p]),
     "fcv_flow_prompt_cond": (c_int32, [POINTER(FcvFlowDims), c_void_p, POINTER(c_int32),

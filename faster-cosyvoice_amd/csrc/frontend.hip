@@ -16,6 +16,7 @@
 // depend on what it is packed with.  The per-document prefix sums travel by value in the kernel
 // arguments (DocTables, at most kMaxDocs documents), so a call needs no host-to-device copy and
 // no synchronisation.
+#include <mutex>
 #include <string>
 
 #include "../../include/fcv_flow.h"
@@ -340,6 +341,123 @@ int check_dims(const FcvFlowDims* dims) {
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// Checks one token-features call and builds its per-document tables (tab.a: token prefix sums,
+// tab.b: output-token prefix sums) and its output token count.
+int prepare_token_features(const FcvFlowDims* dims, const FcvFlowWeights* weights,
+                           const int32_t* tokens, const int32_t* cu_tokens_host,
+                           const int32_t* finalize_host, int32_t n_docs, float* mu_out,
+                           DocTables* tab, int* n_out) {
+  if (int rc = check_dims(dims)) return rc;
+  const FcvFlowDims& d = *dims;
+  FCV_CHECK(weights && weights->embed && weights->la1_w && weights->la1_b && weights->la2_w &&
+                weights->la2_b,
+            FCV_ERR_INVALID, "null weight pointer");
+  const FcvFlowWeights& w = *weights;
+  FCV_CHECK(aligned16(w.embed) && aligned16(w.la1_w) && aligned16(w.la1_b) &&
+                aligned16(w.la2_w) && aligned16(w.la2_b),
+            FCV_ERR_INVALID, "weights must be 16-byte aligned");
+  FCV_CHECK(tokens && cu_tokens_host && mu_out, FCV_ERR_INVALID, "null argument");
+  FCV_CHECK(aligned16(mu_out), FCV_ERR_INVALID, "mu_out must be 16-byte aligned");
+  FCV_CHECK(n_docs >= 1 && n_docs <= kMaxDocs, FCV_ERR_INVALID,
+            "n_docs must be in [1, " + std::to_string(kMaxDocs) + "]");
+  FCV_CHECK(cu_tokens_host[0] == 0, FCV_ERR_INVALID, "cu_tokens[0] must be 0");
+  tab->a[0] = tab->b[0] = 0;
+  for (int i = 0; i < n_docs; ++i) {
+    const long len = (long)cu_tokens_host[i + 1] - cu_tokens_host[i];
+    FCV_CHECK(len >= 1, FCV_ERR_INVALID, "document " + std::to_string(i) + " has no tokens");
+    const bool fin = finalize_host == nullptr || finalize_host[i] != 0;
+    FCV_CHECK(fin || len > d.lookahead, FCV_ERR_INVALID,
+              "document " + std::to_string(i) + " is not finalized and has no more tokens than "
+              "the lookahead");
+    const long out = tab->b[i] + len - (fin ? 0 : d.lookahead);
+    FCV_CHECK(cu_tokens_host[i + 1] <= (1 << 24) && out <= (1 << 24), FCV_ERR_INVALID,
+              "too many tokens");
+    tab->a[i + 1] = cu_tokens_host[i + 1];
+    tab->b[i + 1] = (int32_t)out;
+  }
+  *n_out = tab->b[n_docs];
+  return FCV_OK;
+}
+
+// The three kernels of a checked call, with the workspace at `ws` (flow_layout of n_out).
+int launch_token_features(const FcvFlowDims& d, const FcvFlowWeights& w, const int32_t* tokens,
+                          const DocTables& tab, int n_docs, int n_out, float* mu_out, char* ws,
+                          hipStream_t stream) {
+  const FlowLayout L = flow_layout(d, n_out);
+  float* hid = reinterpret_cast<float*>(ws + L.hidden);
+  float* part = reinterpret_cast<float*>(ws + L.part);
+  const int t_tiles = (n_out + kTileT - 1) / kTileT;
+  hipLaunchKernelGGL(lookahead_conv1_kernel, dim3(t_tiles, d.channels / kTileC), dim3(256), 0,
+                     stream, tokens, tab, n_docs, n_out, w.embed, d.vocab, w.la1_w, w.la1_b,
+                     d.channels, d.lookahead + 1, hid);
+  FCV_HIP(hipGetLastError());
+  hipLaunchKernelGGL(lookahead_conv2_kernel, dim3(t_tiles, kSplit), dim3(256), 0, stream, hid,
+                     tab, n_docs, n_out, w.la2_w, d.channels, part);
+  FCV_HIP(hipGetLastError());
+  const long items = (long)n_out * (kFeat / 4);
+  hipLaunchKernelGGL(lookahead_finish_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0,
+                     stream, part, tokens, tab, n_docs, n_out, w.embed, d.vocab, w.la2_b,
+                     d.token_mel_ratio, mu_out);
+  FCV_HIP(hipGetLastError());
+  return FCV_OK;
+}
+
+}  // namespace
+
+// ---- scratch of fcv_flow_token_features_noalloc ----------------------------------------------
+// The workspace of the no-allocation entry point: a file-scope device array, one copy per GPU,
+// held from module load until the process ends.  Every no-allocation call on a GPU uses that
+// GPU's copy (calls that overlap on one GPU race on it).  Host code never passes the array's
+// name to a kernel (on the host it is a stand-in, not a device address): scratch_for looks up
+// each device's address once, with that device current, and the launches take that address.
+// Nothing in it needs clearing: conv1 writes every hidden row a call reads and conv2 every
+// partial sum the finishing kernel reads.
+constexpr size_t kScratchBytes = FCV_FLOW_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+char* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// output tokens a call can take within the scratch at these dims
+int noalloc_max_tokens(const FcvFlowDims& d) {
+  int lo = 0, hi = 1 << 24;
+  while (lo < hi) {
+    const int mid = lo + (hi - lo + 1) / 2;
+    if (flow_layout(d, mid).total <= kScratchBytes) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Device address of `scratch` on the device `stream` belongs to (looked up once per device).
+int scratch_for(hipStream_t stream, char** out) {
+  int dev = 0;
+  if (stream) {
+    FCV_HIP(hipStreamGetDevice(stream, &dev));
+  } else {
+    FCV_HIP(hipGetDevice(&dev));
+  }
+  FCV_CHECK(dev >= 0 && dev < kMaxScratchDevices, FCV_ERR_RUNTIME,
+            "device index " + std::to_string(dev) + " out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    int current = 0;
+    FCV_HIP(hipGetDevice(&current));
+    if (current != dev) FCV_HIP(hipSetDevice(dev));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (current != dev) (void)hipSetDevice(current);
+    if (e != hipSuccess)
+      return fail(FCV_ERR_RUNTIME, std::string("hipGetSymbolAddress(scratch): ") +
+                                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<char*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return FCV_OK;
+}
+
 }  // namespace
 }  // namespace fcv
 
@@ -356,58 +474,42 @@ int fcv_flow_token_features(const FcvFlowDims* dims, const FcvFlowWeights* weigh
                             const int32_t* tokens, const int32_t* cu_tokens_host,
                             const int32_t* finalize_host, int32_t n_docs, float* mu_out,
                             void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  if (int rc = fcv::check_dims(dims)) return rc;
-  const FcvFlowDims& d = *dims;
-  FCV_CHECK(weights && weights->embed && weights->la1_w && weights->la1_b && weights->la2_w &&
-                weights->la2_b,
-            FCV_ERR_INVALID, "null weight pointer");
-  const FcvFlowWeights& w = *weights;
-  FCV_CHECK(fcv::aligned16(w.embed) && fcv::aligned16(w.la1_w) && fcv::aligned16(w.la1_b) &&
-                fcv::aligned16(w.la2_w) && fcv::aligned16(w.la2_b),
-            FCV_ERR_INVALID, "weights must be 16-byte aligned");
-  FCV_CHECK(tokens && cu_tokens_host && mu_out && workspace, FCV_ERR_INVALID, "null argument");
-  FCV_CHECK(fcv::aligned16(mu_out), FCV_ERR_INVALID, "mu_out must be 16-byte aligned");
-  FCV_CHECK(n_docs >= 1 && n_docs <= fcv::kMaxDocs, FCV_ERR_INVALID,
-            "n_docs must be in [1, " + std::to_string(fcv::kMaxDocs) + "]");
-  FCV_CHECK(cu_tokens_host[0] == 0, FCV_ERR_INVALID, "cu_tokens[0] must be 0");
-  fcv::DocTables tab{};  // a: token prefix sums, b: output-token prefix sums
-  for (int i = 0; i < n_docs; ++i) {
-    const long len = (long)cu_tokens_host[i + 1] - cu_tokens_host[i];
-    FCV_CHECK(len >= 1, FCV_ERR_INVALID, "document " + std::to_string(i) + " has no tokens");
-    const bool fin = finalize_host == nullptr || finalize_host[i] != 0;
-    FCV_CHECK(fin || len > d.lookahead, FCV_ERR_INVALID,
-              "document " + std::to_string(i) + " is not finalized and has no more tokens than "
-              "the lookahead");
-    const long out = tab.b[i] + len - (fin ? 0 : d.lookahead);
-    FCV_CHECK(cu_tokens_host[i + 1] <= (1 << 24) && out <= (1 << 24), FCV_ERR_INVALID,
-              "too many tokens");
-    tab.a[i + 1] = cu_tokens_host[i + 1];
-    tab.b[i + 1] = (int32_t)out;
-  }
-  const int n_out = tab.b[n_docs];
-  const fcv::FlowLayout L = fcv::flow_layout(d, n_out);
+  fcv::DocTables tab{};
+  int n_out = 0;
+  if (int rc = fcv::prepare_token_features(dims, weights, tokens, cu_tokens_host, finalize_host,
+                                           n_docs, mu_out, &tab, &n_out))
+    return rc;
+  FCV_CHECK(workspace, FCV_ERR_INVALID, "null workspace");
+  const fcv::FlowLayout L = fcv::flow_layout(*dims, n_out);
   FCV_CHECK(workspace_bytes >= L.total, FCV_ERR_INVALID,
             "workspace too small: need " + std::to_string(L.total) + " bytes");
   FCV_CHECK(reinterpret_cast<uintptr_t>(workspace) % fcv::kAlign == 0, FCV_ERR_INVALID,
             "workspace must be 256-byte aligned");
+  return fcv::launch_token_features(*dims, *weights, tokens, tab, n_docs, n_out, mu_out,
+                                    static_cast<char*>(workspace), stream);
+}
 
-  char* ws = static_cast<char*>(workspace);
-  float* hid = reinterpret_cast<float*>(ws + L.hidden);
-  float* part = reinterpret_cast<float*>(ws + L.part);
-  const int t_tiles = (n_out + fcv::kTileT - 1) / fcv::kTileT;
-  hipLaunchKernelGGL(fcv::lookahead_conv1_kernel, dim3(t_tiles, d.channels / fcv::kTileC),
-                     dim3(256), 0, stream, tokens, tab, n_docs, n_out, w.embed, d.vocab, w.la1_w,
-                     w.la1_b, d.channels, d.lookahead + 1, hid);
-  FCV_HIP(hipGetLastError());
-  hipLaunchKernelGGL(fcv::lookahead_conv2_kernel, dim3(t_tiles, fcv::kSplit), dim3(256), 0,
-                     stream, hid, tab, n_docs, n_out, w.la2_w, d.channels, part);
-  FCV_HIP(hipGetLastError());
-  const long items = (long)n_out * (fcv::kFeat / 4);
-  hipLaunchKernelGGL(fcv::lookahead_finish_kernel, dim3((unsigned)((items + 255) / 256)),
-                     dim3(256), 0, stream, part, tokens, tab, n_docs, n_out, w.embed, d.vocab,
-                     w.la2_b, d.token_mel_ratio, mu_out);
-  FCV_HIP(hipGetLastError());
-  return FCV_OK;
+int fcv_flow_token_features_noalloc(const FcvFlowDims* dims, const FcvFlowWeights* weights,
+                                    const int32_t* tokens, const int32_t* cu_tokens_host,
+                                    const int32_t* finalize_host, int32_t n_docs, float* mu_out,
+                                    hipStream_t stream) {
+  fcv::DocTables tab{};
+  int n_out = 0;
+  if (int rc = fcv::prepare_token_features(dims, weights, tokens, cu_tokens_host, finalize_host,
+                                           n_docs, mu_out, &tab, &n_out))
+    return rc;
+  const fcv::FlowLayout L = fcv::flow_layout(*dims, n_out);
+  FCV_CHECK(L.total <= fcv::kScratchBytes, FCV_ERR_INVALID,
+            std::to_string(n_out) + " output tokens need " + std::to_string(L.total) +
+                " bytes of scratch; the no-allocation entry point holds " +
+                std::to_string(fcv::kScratchBytes) + " (at most " +
+                std::to_string(fcv::noalloc_max_tokens(*dims)) +
+                " output tokens per call at these dims): split the batch or pass a workspace "
+                "to fcv_flow_token_features");
+  char* ws = nullptr;
+  if (int rc = fcv::scratch_for(stream, &ws)) return rc;
+  return fcv::launch_token_features(*dims, *weights, tokens, tab, n_docs, n_out, mu_out, ws,
+                                    stream);
 }
 
 int fcv_flow_speaker(const FcvFlowDims* dims, const FcvFlowWeights* weights, const float* xvec,

@@ -80,6 +80,20 @@ int fcv_flow_token_features(const FcvFlowDims* dims, const FcvFlowWeights* weigh
                             const int32_t* finalize_host, int32_t n_docs, float* mu_out,
                             void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* fcv_flow_token_features without a workspace argument: no counterpart in the reference.  It is
+ * for callers that cannot allocate device memory (code under hipGraph capture, serving loops or
+ * harnesses that forbid hipMalloc).  Same inputs, outputs and results as
+ * fcv_flow_token_features; the workspace is the library's own 32 MiB device array, one copy per
+ * GPU, held until the process ends, so a call takes at most FCV_FLOW_NOALLOC_SCRATCH_BYTES of
+ * workspace (fcv_flow_workspace_bytes): 5041 output tokens at the builders.py dims.  Larger
+ * calls fail with FCV_ERR_INVALID.  The call allocates nothing.  Calls that overlap on one GPU
+ * (on different streams or threads) race on the array: issue them on one stream. */
+#define FCV_FLOW_NOALLOC_SCRATCH_BYTES (32u << 20)
+int fcv_flow_token_features_noalloc(const FcvFlowDims* dims, const FcvFlowWeights* weights,
+                                    const int32_t* tokens, const int32_t* cu_tokens_host,
+                                    const int32_t* finalize_host, int32_t n_docs, float* mu_out,
+                                    hipStream_t stream);
+
 /* Speaker path (flashinfer_flow.py:145-146, :230-231): spks_out[n] = spk_w . (xvec[n] /
  * max(||xvec[n]||_2, 1e-12)) + spk_b.  xvec: [n][spk_dim]; spks_out: [n][feat_dim]. */
 int fcv_flow_speaker(const FcvFlowDims* dims, const FcvFlowWeights* weights, const float* xvec,
