@@ -293,6 +293,81 @@ def token2wav_leg(fcv, est, batch, dev) -> dict:
             "timing": "wall clock with torch.cuda.synchronize() on both sides, best of 2"}
 
 
+def _group_caps(fcv, b) -> tuple:
+    """Capacity bucket of each request group the solver makes of batch `b`."""
+    groups = fcv.solver.request_groups(b.lengths, fcv.solver.default_concurrency(b.n_requests))
+    return tuple(fcv.solver.capacity_bucket(2 * sum(b.lengths[i] for i in g), 2 * len(g))
+                 for g in groups)
+
+
+def _fresh_layouts(fcv, est, base, variants, K: int) -> dict:
+    """Solve `base` twice (each request group's capacity bucket gets its graph on the second),
+    then time each variant (a layout never seen before, in the same buckets) replayed from
+    those graphs and solved eagerly on exact plans."""
+    import torch
+
+    def solve(b, graph, bucketed):
+        return fcv.solve_euler_packed(est, b.noise, b.mu, b.cond, b.spks, b.lengths, n_steps=K,
+                                      streaming=b.streaming, use_graph=graph, bucketed=bucketed)
+
+    lanes = est.lanes(len(_group_caps(fcv, base)))
+    captures = lambda: sum(r.graph_stats()[1] for r in lanes)
+    solve(base, True, True)
+    solve(base, True, True)  # the buckets' graphs are captured here
+    captured = captures()
+
+    def timed(b, graph, bucketed):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        solve(b, graph, bucketed)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / K
+
+    replay = [timed(v, True, True) for v in variants]
+    new_captures = captures() - captured
+    eager = [timed(v, False, False) for v in variants]
+    med = lambda xs: sorted(xs)[len(xs) // 2]
+    return {"request_groups": len(lanes), "capacities": [list(c) for c in _group_caps(fcv, base)],
+            "layouts": len(variants), "rows": [v.rows for v in variants],
+            "captures_during_replays": new_captures,
+            "replay_ms_per_step": round(med(replay), 4), "eager_ms_per_step": round(med(eager), 4)}
+
+
+def fresh_layout_leg(fcv, est, batch, K: int, n_layouts: int = 4) -> dict:
+    """K-step solves of layouts the solver has never seen, replayed from the graphs captured
+    for their capacity buckets on another layout, against eager exact plans of the same layouts
+    (wall clock between device synchronisations, median over the layouts):
+    (a) the workload with every request length moved by a seeded -20..20 frames, kept when each
+    request group stays in its bucket (the default two concurrent groups);
+    (b) one request (a single streaming session for the chunk-causal workload) of a new length
+    each solve, all in one bucket."""
+    import numpy as np
+    out = {"what": "graph replay of new layouts in captured capacity buckets vs eager exact "
+                   "plans", "timing": "median over the layouts; wall clock with "
+                   "torch.cuda.synchronize() on both sides"}
+    rng = np.random.Generator(np.random.PCG64(7))
+    variants = []
+    for _ in range(200):
+        lengths = [max(8, n + int(d)) for n, d in zip(batch.lengths,
+                                                      rng.integers(-20, 21, batch.n_requests))]
+        prompts = [min(p, n - 1) for p, n in zip(batch.prompt_lengths, lengths)]
+        v = fcv.synthetic.make_batch("fresh", lengths, prompts, seed=int(rng.integers(1 << 30)),
+                                     streaming=batch.streaming)
+        if _group_caps(fcv, v) == _group_caps(fcv, batch):
+            variants.append(v)
+        if len(variants) == n_layouts:
+            break
+    if variants:
+        out["workload"] = _fresh_layouts(fcv, est, batch, variants, K)
+    # single request: 60 new frames after prompts of 295..320 frames (all in one bucket)
+    single = [fcv.synthetic.make_batch("single", [p + 60], [p], seed=100 + p,
+                                       streaming=batch.streaming)
+              for p in (300, 295, 305, 312, 320)]
+    assert all(_group_caps(fcv, v) == _group_caps(fcv, single[0]) for v in single)
+    out["single_request"] = _fresh_layouts(fcv, est, single[0], single[1:], K)
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -310,6 +385,8 @@ def main() -> int:
     ap.add_argument("--no-token2wav", action="store_true",
                     help="skip the end-to-end tokens -> waveform leg")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one (no hipGraph)")
+    ap.add_argument("--no-fresh-layouts", action="store_true",
+                    help="skip the leg that solves new layouts through the bucket's graph")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -418,6 +495,11 @@ def main() -> int:
             if vals:
                 breakdown[name] = round(sum(vals) / len(vals), 4)
 
+    fresh = None
+    if not args.no_fresh_layouts:
+        log("[bench] new layouts through the capacity bucket's graph")
+        fresh = fresh_layout_leg(fcv, est, batch, K)
+
     frontend = None
     if not args.no_frontend:
         log("[bench] flow front-end (tokens -> packed mu rows)")
@@ -491,6 +573,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "stage_ms": breakdown,
+        "fresh_layouts": fresh,
         "frontend": frontend,
         "hift": hift,
         "token2wav": t2w,

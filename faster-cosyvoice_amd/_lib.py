@@ -74,6 +74,9 @@ SIGNATURES = {
     "fcv_dit_workspace_bytes": (c_size_t, [c_void_p, c_int32, c_int32]),
     "fcv_dit_plan": (c_int32, [c_void_p, POINTER(c_int32), c_int32, c_int32, c_int32, c_void_p,
                                c_size_t, c_void_p]),
+    "fcv_dit_plan_capacity": (c_int32, [c_void_p, POINTER(c_int32), c_int32, c_int32, c_int32,
+                                        c_int32, c_int32, c_void_p, c_size_t, c_void_p]),
+    "fcv_dit_graph_stats": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32)]),
     "fcv_dit_plan_info": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32),
                                     POINTER(c_int32)]),
     "fcv_dit_forward": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -49,12 +49,14 @@ __device__ __forceinline__ float half_sum(float v) {
 __global__ __launch_bounds__(256, 2) void attention_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ VT,
     bf16* __restrict__ O, const int32_t* __restrict__ dstart, const int32_t* __restrict__ dlen,
-    const int32_t* __restrict__ tiles, int rows, int rp, int heads, int chunk, float scale_log2) {
+    const int32_t* __restrict__ tiles, int rp, int heads, int chunk, float scale_log2,
+    const int32_t* __restrict__ tiles_live) {
   __shared__ __attribute__((aligned(16))) bf16 sK[2][TK][LDP];
   __shared__ __attribute__((aligned(16))) bf16 sV[2][HD][LDP];
 
   const int tile = blockIdx.x / heads;
   const int head = blockIdx.x % heads;
+  if (tiles_live && tile >= *tiles_live) return;  // past the live tiles of a capacity grid
   const int doc = tiles[2 * tile];
   const int q0 = tiles[2 * tile + 1];
   const int doc_start = dstart[doc];
@@ -78,8 +80,8 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
   const int key_lim =
       chunk > 0 ? min(kv_end, doc_start + (max(q_pos, 0) / chunk + 1) * chunk) : kv_end;
 
-  const bf16* Qh = Q + (long)head * rows * HD;
-  const bf16* Kh = K + (long)head * rows * HD;
+  const bf16* Qh = Q + (long)head * rp * HD;
+  const bf16* Kh = K + (long)head * rp * HD;
   const bf16* Vh = VT + (long)head * HD * rp;
 
   // Q^T fragments (B operand): query ql, dims 16*ks + 8*hl + 0..7
@@ -93,7 +95,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
 
   // tile loaders: each thread moves 2 x 16 bytes of K and 2 x 16 bytes of V^T, through raw
   // buffer loads over this head's K rows and V^T block: 32-bit offsets, and chunks past the end
-  // read as zeros (keys past `rows` are masked anyway).  A V^T chunk holds 8 keys from a
+  // read as zeros (keys past the document are masked anyway).  A V^T chunk holds 8 keys from a
   // multiple of 8 (documents start 8-aligned); keys at or past kv_end are zeroed when the chunk
   // is stashed.  The next tile is fetched unconditionally (the surplus tile lands in the buffer
   // no later iteration reads), so the compiler never waits on a load before the stash that
@@ -101,7 +103,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
   const int lr = tid >> 3;         // 0..31
   const int lc = (tid & 7) * 8;    // 0..56
   const __amdgpu_buffer_rsrc_t k_rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(Kh), (short)0, rows * HD * 2, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(Kh), (short)0, rp * HD * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t v_rsrc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(Vh), (short)0, HD * rp * 2, 0x00020000);
   const uint32_t k_lane = (uint32_t)(lr * HD + lc) * 2, v_lane = (uint32_t)(lr * rp) * 2;
@@ -253,15 +255,14 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
 
 hipError_t attention_varlen(const bf16* q, const bf16* k, const bf16* vt, bf16* o,
                             const int32_t* doc_start, const int32_t* doc_len,
-                            const int32_t* tiles, int n_tiles, int rows, int rp, int heads,
-                            int chunk, hipStream_t stream) {
+                            const int32_t* tiles, int n_tiles, int rp, int heads, int chunk,
+                            hipStream_t stream, const int32_t* tiles_live) {
   if (n_tiles <= 0) return hipSuccess;
   // per-head K rows and V^T blocks are addressed by 32-bit buffer offsets
-  if ((long)rows * HD * 2 >= (1L << 31) || (long)HD * rp * 2 >= (1L << 31) || rp < rows)
-    return hipErrorInvalidValue;
+  if ((long)HD * rp * 2 >= (1L << 31)) return hipErrorInvalidValue;
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // 64^-0.5 * log2(e)
   hipLaunchKernelGGL(attention_kernel, dim3(n_tiles * heads), dim3(256), 0, stream, q, k, vt, o,
-                     doc_start, doc_len, tiles, rows, rp, heads, chunk, scale_log2);
+                     doc_start, doc_len, tiles, rp, heads, chunk, scale_log2, tiles_live);
   return hipGetLastError();
 }
 

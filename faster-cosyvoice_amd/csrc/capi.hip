@@ -1,6 +1,7 @@
 // C ABI of libfcvdit.so: handle, layout planning, the packed DiT forward, the CFG Euler
 // step and the hipGraph-captured solve.  See include/fcv_dit.h for the contract.
 #include <algorithm>
+#include <climits>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -33,13 +34,15 @@ constexpr int kMaxSteps = 64;
 // (a 10-step solve reads the 281 MB of AdaLN weights once)
 constexpr int kModGroup = 16;
 constexpr int kRowTile = 128;
+constexpr size_t kGraphPool = 4;   // captured solves kept per handle (least recently used goes)
+constexpr size_t kSeenKeys = 8;    // solve keys remembered for the capture-on-second-sight rule
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct Layout {
   // byte offsets inside the workspace
   size_t h, nbuf, obuf, q, k, vt, u, ain, vbuf;
-  size_t docid, pos, ext_row, docid_ext, pos_ext, cu_int, lens, cu_ext, tiles;
+  size_t docid, pos, ext_row, docid_ext, pos_ext, cu_int, lens, cu_ext, tiles, live;
   size_t mod, tsin, t1, t2, tbuf;
   size_t total;
 };
@@ -47,11 +50,15 @@ struct Layout {
 // Internal rows: every document starts at a multiple of 8 rows (at most 7 pad rows each), so
 // attention key tiles and 16-byte V^T loads are aligned to the document start.
 long internal_rows_bound(long rows, long n_docs) { return rows + 7 * n_docs; }
+long tiles_bound(long rows, long n_docs) {
+  return internal_rows_bound(rows, n_docs) / fcv::kAttnTileQ + n_docs + 1;
+}
 
+// Workspace of a capacity: at most `rows` caller rows in at most `n_docs` documents.
 Layout make_layout(const FcvDitDims& d, long rows, long n_docs) {
   const long ri = internal_rows_bound(rows, n_docs);
   const long rp = align_up(std::max<long>(ri, 1), kRowTile);
-  const long n_tiles = ri / fcv::kAttnTileQ + n_docs + 1;
+  const long n_tiles = tiles_bound(rows, n_docs);
   const long mod_width = (long)d.depth * 6 * d.dim + 2L * d.dim;
   const long nd = std::max<long>(n_docs, 1);
   Layout L{};
@@ -79,6 +86,7 @@ Layout make_layout(const FcvDitDims& d, long rows, long n_docs) {
   L.lens = take(nd * 4);
   L.cu_ext = take((nd + 1) * 4);
   L.tiles = take(n_tiles * 2 * 4);
+  L.live = take(4 * 4);
   const long nt = std::max<long>(nd, kModGroup);  // time rows: per document, or a step group
   L.mod = take(nt * mod_width * 4);
   L.tsin = take(nt * 256 * 2);
@@ -96,10 +104,14 @@ struct FcvDit {
   FcvDitWeights w{};
   long mod_width = 0;
 
-  // plan: `rows` caller rows (cu_host); `rows_int` internal 8-aligned rows, rp >= rows_int
+  // plan: `rows` caller rows (cu_host); `rows_int` internal 8-aligned rows.  The capacity
+  // (rows_cap caller rows in docs_cap documents) sizes the workspace layout and every grid:
+  // rint_cap internal rows, tiles_cap attention tiles, rc_cap caller rows per CFG half, rp the
+  // row pitch of q, k and V^T.  The live counts sit in the workspace (Layout::live).
   bool planned = false;
   unsigned long generation = 0;
   int rows = 0, rows_int = 0, rp = 0, n_docs = 0, n_tiles = 0, mask_mode = 0, chunk = 0;
+  int rows_cap = 0, docs_cap = 0, rint_cap = 0, tiles_cap = 0, rc_cap = 0;
   std::vector<int32_t> cu_host;
   char* ws = nullptr;
   size_t ws_bytes = 0;
@@ -112,18 +124,24 @@ struct FcvDit {
   int probe_repeat = 1;
   std::vector<hipEvent_t> probe_events;
 
-  // graph cache: the captured solve and its key; seen_key is the previous solve's key
-  hipGraphExec_t graph_exec = nullptr;
-  std::vector<uintptr_t> graph_key;
-  std::vector<uintptr_t> seen_key;
+  // graph pool: captured solves by key (capacity, mask, workspace, solver buffers, schedule),
+  // most recently used first; seen: keys of recent solves (a key is captured on its second)
+  struct Graph {
+    std::vector<uintptr_t> key;
+    hipGraphExec_t exec;
+  };
+  std::vector<Graph> graphs;
+  std::vector<std::vector<uintptr_t>> seen;
+  long captures = 0;  // solves captured into a graph over the handle's life
 
   template <class T>
   T* at(size_t off) const { return reinterpret_cast<T*>(ws + off); }
+  const int32_t* live() const { return at<int32_t>(L.live); }
 
   void drop_graph() {
-    if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
-    graph_exec = nullptr;
-    graph_key.clear();
+    for (Graph& g : graphs) (void)hipGraphExecDestroy(g.exec);
+    graphs.clear();
+    seen.clear();
   }
 
   void drop_probe() {
@@ -200,7 +218,10 @@ int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, co
                const float* mod, long mod_stride, float* v_out, hipStream_t s) {
   const FcvDitDims& d = m->dims;
   const FcvDitWeights& w = m->w;
-  const int R = m->rows_int, D = d.dim, F = d.ff_dim, mel = d.mel_dim;
+  // grids cover the plan's capacity; the kernels read the live counts
+  const int R = m->rint_cap, D = d.dim, F = d.ff_dim, mel = d.mel_dim;
+  const int32_t* live_rows = m->live() + fcv::kLiveRows;
+  const int32_t* live_tiles = m->live() + fcv::kLiveTiles;
   auto B = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
 
   float* h = m->at<float>(m->L.h);
@@ -219,19 +240,19 @@ int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, co
   int32_t* tiles = m->at<int32_t>(m->L.tiles);
 
   // input projection + causal conv position embedding (InputEmbedding dit.py:84-98)
-  FCV_HIP(fcv::pack_inputs(x, cond, mu, spks, docid, ext_row, R, mel, ain, s));
+  FCV_HIP(fcv::pack_inputs(x, cond, mu, spks, docid, ext_row, R, mel, ain, s, live_rows));
   FCV_HIP(m->probe_begin(FCV_STAGE_IN_PROJ, -1, s));
   for (int rep = m->launches(FCV_STAGE_IN_PROJ, -1); rep > 0; --rep)
     FCV_HIP(fcv::gemm_bias_f32_bf16(ain, 4 * mel, B(w.in_w), 4 * mel, w.in_b, R, D, 4 * mel, h,
-                                    nbuf, D, s));
+                                    nbuf, D, s, live_rows));
   FCV_HIP(m->probe_end(FCV_STAGE_IN_PROJ, -1, s));
   FCV_HIP(m->probe_begin(FCV_STAGE_CONV, -1, s));
   for (int rep = m->launches(FCV_STAGE_CONV, -1); rep > 0; --rep)
     FCV_HIP(fcv::conv_causal_mish(nbuf, D, B(w.conv1_w), w.conv1_b, d.conv_kernel, pos, R, obuf,
-                                  nullptr, s));
+                                  nullptr, s, live_rows));
   FCV_HIP(m->probe_end(FCV_STAGE_CONV, -1, s));
   FCV_HIP(fcv::conv_causal_mish(obuf, D, B(w.conv2_w), w.conv2_b, d.conv_kernel, pos, R,
-                                nullptr, h, s));
+                                nullptr, h, s, live_rows));
 
   // transformer blocks (DiTBlock.forward modules.py:516-530)
   for (int l = 0; l < d.depth; ++l) {
@@ -239,47 +260,48 @@ int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, co
     FCV_HIP(m->probe_begin(FCV_STAGE_LN_MOD, l, s));
     for (int rep = m->launches(FCV_STAGE_LN_MOD, l); rep > 0; --rep)
       FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 0), (int)(base + D),
-                                       docid, nbuf, s));
+                                       docid, nbuf, s, live_rows));
     FCV_HIP(m->probe_end(FCV_STAGE_LN_MOD, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_QKV, l, s));
     for (int rep = m->launches(FCV_STAGE_QKV, l); rep > 0; --rep)
       FCV_HIP(fcv::gemm_qkv_rope(nbuf, D, B(w.qkv_w) + (long)l * 3 * D * D, D,
                                  w.qkv_b + (long)l * 3 * D, R, D, d.heads, pos, w.rope_cos,
-                                 w.rope_sin, d.rope_dim, d.max_pos, q, k, vt, m->rp, s));
+                                 w.rope_sin, d.rope_dim, d.max_pos, q, k, vt, m->rp, s,
+                                 live_rows));
     FCV_HIP(m->probe_end(FCV_STAGE_QKV, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_ATTENTION, l, s));
     for (int rep = m->launches(FCV_STAGE_ATTENTION, l); rep > 0; --rep)
-      FCV_HIP(fcv::attention_varlen(q, k, vt, obuf, cu_int, lens, tiles, m->n_tiles, R, m->rp,
+      FCV_HIP(fcv::attention_varlen(q, k, vt, obuf, cu_int, lens, tiles, m->tiles_cap, m->rp,
                                     d.heads, m->mask_mode == FCV_MASK_CHUNK_CAUSAL ? m->chunk : 0,
-                                    s));
+                                    s, live_tiles));
     FCV_HIP(m->probe_end(FCV_STAGE_ATTENTION, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_OUT_PROJ, l, s));
     FCV_HIP(fcv::gemm_gated_residual(obuf, D, B(w.out_w) + (long)l * D * D, D,
                                      w.out_b + (long)l * D, R, D, D, h, D, mod + base + 2 * D,
-                                     mod_stride, docid, s));
+                                     mod_stride, docid, s, live_rows));
     FCV_HIP(m->probe_end(FCV_STAGE_OUT_PROJ, l, s));
     FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 3 * D),
-                                     (int)(base + 4 * D), docid, nbuf, s));
+                                     (int)(base + 4 * D), docid, nbuf, s, live_rows));
     FCV_HIP(m->probe_begin(FCV_STAGE_FF1, l, s));
     for (int rep = m->launches(FCV_STAGE_FF1, l); rep > 0; --rep)
       FCV_HIP(fcv::gemm_bias_gelu_bf16(nbuf, D, B(w.ff1_w) + (long)l * F * D, D,
-                                       w.ff1_b + (long)l * F, R, F, D, u, F, s));
+                                       w.ff1_b + (long)l * F, R, F, D, u, F, s, live_rows));
     FCV_HIP(m->probe_end(FCV_STAGE_FF1, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_FF2, l, s));
     FCV_HIP(fcv::gemm_gated_residual(u, F, B(w.ff2_w) + (long)l * D * F, F,
                                      w.ff2_b + (long)l * D, R, D, F, h, D, mod + base + 5 * D,
-                                     mod_stride, docid, s));
+                                     mod_stride, docid, s, live_rows));
     FCV_HIP(m->probe_end(FCV_STAGE_FF2, l, s));
   }
 
   // final AdaLN (scale, shift) + proj_out (dit.py:174-175, modules.py:260-265)
   const long fin = (long)d.depth * 6 * D;
   FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(fin + D), (int)fin, docid,
-                                   nbuf, s));
+                                   nbuf, s, live_rows));
   FCV_HIP(m->probe_begin(FCV_STAGE_PROJ_OUT, -1, s));
   for (int rep = m->launches(FCV_STAGE_PROJ_OUT, -1); rep > 0; --rep)
     FCV_HIP(fcv::gemm_bias_f32_rowmap(nbuf, D, B(w.proj_w), D, w.proj_b, R, 128, D, v_out, mel,
-                                      mel, ext_row, s));
+                                      mel, ext_row, s, live_rows));
   FCV_HIP(m->probe_end(FCV_STAGE_PROJ_OUT, -1, s));
   return FCV_OK;
 }
@@ -332,8 +354,9 @@ size_t fcv_dit_workspace_bytes(const FcvDit* dit, int32_t rows, int32_t n_docs) 
   return make_layout(dit->dims, rows, n_docs).total;
 }
 
-int fcv_dit_plan(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask_mode,
-                 int32_t chunk, void* workspace, size_t workspace_bytes, hipStream_t s) {
+int fcv_dit_plan_capacity(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask_mode,
+                          int32_t chunk, int32_t rows_cap, int32_t docs_cap, void* workspace,
+                          size_t workspace_bytes, hipStream_t s) {
   FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
   FCV_CHECK(cu_host && n_docs >= 1, FCV_ERR_INVALID, "need at least one document");
   FCV_CHECK(mask_mode == FCV_MASK_FULL || mask_mode == FCV_MASK_CHUNK_CAUSAL, FCV_ERR_INVALID,
@@ -349,11 +372,16 @@ int fcv_dit_plan(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask
                   std::to_string(m->dims.max_pos));
   }
   const int rows = cu_host[n_docs];
+  FCV_CHECK(rows <= rows_cap && n_docs <= docs_cap, FCV_ERR_INVALID,
+            "layout of " + std::to_string(rows) + " rows in " + std::to_string(n_docs) +
+                " documents exceeds the capacity (" + std::to_string(rows_cap) + " rows, " +
+                std::to_string(docs_cap) + " documents)");
   // the kernels address activations by 32-bit byte offsets within buffer ranges held as an
   // int: the widest row (the FF hidden row in bf16 or the fp32 residual row) times the internal
-  // rows must stay below 2 GB
+  // rows of the capacity must stay below 2 GB
   const long row_bytes = std::max<long>(2L * m->dims.ff_dim, 4L * m->dims.dim);
-  FCV_CHECK(internal_rows_bound(rows, n_docs) * row_bytes < (1L << 31), FCV_ERR_INVALID,
+  FCV_CHECK(align_up(internal_rows_bound(rows_cap, docs_cap), kRowTile) * row_bytes < (1L << 31),
+            FCV_ERR_INVALID,
             "too many rows: (rows + 7 per document) x " + std::to_string(row_bytes) +
                 " bytes must stay below 2 GB");
 
@@ -386,7 +414,7 @@ int fcv_dit_plan(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask
     tiles_host.push_back(t.q0);
   }
 
-  const Layout L = make_layout(m->dims, rows, n_docs);
+  const Layout L = make_layout(m->dims, rows_cap, docs_cap);
   FCV_CHECK(workspace != nullptr, FCV_ERR_INVALID, "null workspace");
   FCV_CHECK(workspace_bytes >= L.total, FCV_ERR_INVALID,
             "workspace too small: need " + std::to_string(L.total) + " bytes, got " +
@@ -394,19 +422,24 @@ int fcv_dit_plan(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask
   FCV_CHECK(reinterpret_cast<uintptr_t>(workspace) % kAlign == 0, FCV_ERR_INVALID,
             "workspace must be 256-byte aligned");
 
-  m->drop_graph();
   m->planned = false;
   m->ws = static_cast<char*>(workspace);
   m->ws_bytes = workspace_bytes;
   m->L = L;
   m->rows = rows;
   m->rows_int = rows_int;
-  m->rp = (int)align_up(std::max(rows_int, 1), kRowTile);
   m->n_docs = n_docs;
   m->n_tiles = (int)tl.size();
   m->mask_mode = mask_mode;
   m->chunk = mask_mode == FCV_MASK_CHUNK_CAUSAL ? chunk : 0;
   m->cu_host.assign(cu_host, cu_host + n_docs + 1);
+  m->rows_cap = rows_cap;
+  m->docs_cap = docs_cap;
+  m->rint_cap = (int)internal_rows_bound(rows_cap, docs_cap);
+  m->tiles_cap = (int)tiles_bound(rows_cap, docs_cap);
+  m->rc_cap = rows_cap / 2;
+  m->rp = (int)align_up(std::max(m->rint_cap, 1), kRowTile);
+  const std::vector<int32_t> live = {rows_int, m->n_tiles, rows / 2, 0};
 
   auto h2d = [&](size_t off, const std::vector<int32_t>& v) {
     return hipMemcpyAsync(m->ws + off, v.data(), v.size() * sizeof(int32_t),
@@ -416,6 +449,7 @@ int fcv_dit_plan(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask
   FCV_HIP(h2d(L.cu_int, cu_int));
   FCV_HIP(h2d(L.lens, lens));
   FCV_HIP(h2d(L.tiles, tiles_host));
+  FCV_HIP(h2d(L.live, live));
   FCV_HIP(fcv::build_row_index(m->at<int32_t>(L.cu_ext), n_docs, rows,
                                m->at<int32_t>(L.docid_ext), m->at<int32_t>(L.pos_ext), s));
   FCV_HIP(fcv::build_aligned_row_index(m->at<int32_t>(L.cu_int), m->at<int32_t>(L.lens),
@@ -425,6 +459,21 @@ int fcv_dit_plan(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask
   FCV_HIP(hipStreamSynchronize(s));
   m->planned = true;
   m->generation++;
+  return FCV_OK;
+}
+
+int fcv_dit_plan(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int32_t mask_mode,
+                 int32_t chunk, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
+  FCV_CHECK(cu_host && n_docs >= 1, FCV_ERR_INVALID, "need at least one document");
+  return fcv_dit_plan_capacity(m, cu_host, n_docs, mask_mode, chunk, cu_host[n_docs], n_docs,
+                               workspace, workspace_bytes, s);
+}
+
+int fcv_dit_graph_stats(const FcvDit* m, int32_t* pooled, int32_t* captures) {
+  FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
+  if (pooled) *pooled = (int32_t)m->graphs.size();
+  if (captures) *captures = (int32_t)std::min<long>(m->captures, INT32_MAX);
   return FCV_OK;
 }
 
@@ -480,7 +529,7 @@ int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const
 
   float* tbuf = m->at<float>(m->L.tbuf);
   float* vbuf = m->at<float>(m->L.vbuf);
-  const int rcond = m->rows / 2, mel = m->dims.mel_dim;
+  const int mel = m->dims.mel_dim;
   FCV_HIP(hipMemcpyAsync(tbuf, t_host, n_steps * sizeof(float), hipMemcpyHostToDevice, s));
 
   auto body = [&]() -> int {
@@ -496,14 +545,19 @@ int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const
                           vbuf, s);
       if (r != FCV_OK) return r;
       FCV_HIP(m->probe_begin(FCV_STAGE_EULER, -1, s));
-      FCV_HIP(fcv::euler_cfg_update(x, vbuf, rcond, mel, dt_host[step], cfg, s));
+      FCV_HIP(fcv::euler_cfg_update(x, vbuf, m->rc_cap, mel, dt_host[step], cfg, s,
+                                    m->live() + fcv::kLiveHalfRows));
       FCV_HIP(m->probe_end(FCV_STAGE_EULER, -1, s));
     }
     return FCV_OK;
   };
-  // what a captured loop bakes in: the plan, the buffers and the schedule (t is read from tbuf)
-  std::vector<uintptr_t> key = {m->generation, (uintptr_t)x, (uintptr_t)mu, (uintptr_t)cond,
-                                (uintptr_t)spks, (uintptr_t)n_steps};
+  // What a captured loop bakes in: the capacity (workspace offsets and grids), the mask, the
+  // workspace and solver buffers, and the schedule (t is read from tbuf).  The layout itself is
+  // read from the workspace at run time, so any layout planned into the same capacity replays.
+  std::vector<uintptr_t> key = {(uintptr_t)m->rows_cap, (uintptr_t)m->docs_cap,
+                                (uintptr_t)m->mask_mode, (uintptr_t)m->chunk, (uintptr_t)m->ws,
+                                (uintptr_t)x, (uintptr_t)mu, (uintptr_t)cond, (uintptr_t)spks,
+                                (uintptr_t)n_steps};
   uint32_t bits;
   std::memcpy(&bits, &cfg, 4);
   key.push_back(bits);
@@ -511,15 +565,19 @@ int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const
     std::memcpy(&bits, &dt_host[i], 4);
     key.push_back(bits);
   }
-  const bool cached = m->graph_exec && key == m->graph_key;
-  // Capturing and instantiating the loop costs more than running it once eagerly, so a key is
-  // captured on its second solve: a layout used once (a streaming step) never pays for a capture.
-  if (!use_graph || (!cached && key != m->seen_key)) {
-    m->seen_key = key;
-    return body();
-  }
-  if (!cached) {
-    m->drop_graph();
+  if (!use_graph) return body();
+  auto hit = std::find_if(m->graphs.begin(), m->graphs.end(),
+                          [&](const FcvDit::Graph& g) { return g.key == key; });
+  if (hit == m->graphs.end()) {
+    // Capturing and instantiating the loop costs more than running it once eagerly, so a key is
+    // captured on its second solve: a capacity used once never pays for a capture.
+    auto seen = std::find(m->seen.begin(), m->seen.end(), key);
+    if (seen == m->seen.end()) {
+      m->seen.insert(m->seen.begin(), key);
+      if (m->seen.size() > kSeenKeys) m->seen.pop_back();
+      return body();
+    }
+    m->seen.erase(seen);
     FCV_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     int r = body();
     hipGraph_t graph = nullptr;
@@ -530,15 +588,21 @@ int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const
     }
     if (e != hipSuccess)
       return fail(FCV_ERR_RUNTIME, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
-    e = hipGraphInstantiate(&m->graph_exec, graph, nullptr, nullptr, 0);
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
-    if (e != hipSuccess) {
-      m->graph_exec = nullptr;
+    if (e != hipSuccess)
       return fail(FCV_ERR_RUNTIME, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    if (m->graphs.size() >= kGraphPool) {
+      (void)hipGraphExecDestroy(m->graphs.back().exec);
+      m->graphs.pop_back();
     }
-    m->graph_key = key;
+    m->graphs.insert(m->graphs.begin(), FcvDit::Graph{key, exec});
+    m->captures++;
+  } else if (hit != m->graphs.begin()) {
+    std::rotate(m->graphs.begin(), hit, hit + 1);  // most recently used first
   }
-  FCV_HIP(hipGraphLaunch(m->graph_exec, s));
+  FCV_HIP(hipGraphLaunch(m->graphs.front().exec, s));
   return FCV_OK;
 }
 

@@ -35,12 +35,15 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
                                                       const float* __restrict__ bias, int taps,
                                                       const int32_t* __restrict__ pos, int rows,
                                                       bf16* __restrict__ out_bf16,
-                                                      float* __restrict__ h) {
+                                                      float* __restrict__ h,
+                                                      const int32_t* __restrict__ rows_live) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM_BYTES];
   bf16 (*sX)[LDP] = reinterpret_cast<bf16 (*)[LDP]>(smem);
   bf16 (*sW)[CG][LDP] = reinterpret_cast<bf16 (*)[CG][LDP]>(smem + X_BYTES);
 
+  if (rows_live) rows = *rows_live;  // live rows of a capacity-sized grid
   const int m0 = blockIdx.x * TM;
+  if (m0 >= rows) return;
   const int g = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -150,12 +153,12 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
 
 hipError_t conv_causal_mish(const bf16* x, int C, const bf16* w, const float* bias, int taps,
                             const int32_t* pos, int rows, bf16* out_bf16, float* h,
-                            hipStream_t stream) {
+                            hipStream_t stream, const int32_t* rows_live) {
   if (rows <= 0) return hipSuccess;
   if (taps < 1 || taps > MAX_TAPS || C % CG != 0) return hipErrorInvalidValue;
   dim3 grid((rows + TM - 1) / TM, C / CG);
   hipLaunchKernelGGL(conv_kernel, grid, dim3(256), 0, stream, x, C, w, bias, taps, pos, rows,
-                     out_bf16, h);
+                     out_bf16, h, rows_live);
   return hipGetLastError();
 }
 

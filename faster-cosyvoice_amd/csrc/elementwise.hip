@@ -18,9 +18,11 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float* __restrict__ h
                                                      long mod_stride, int shift_off,
                                                      int scale_off,
                                                      const int32_t* __restrict__ docid,
-                                                     bf16* __restrict__ out) {
+                                                     bf16* __restrict__ out,
+                                                     const int32_t* __restrict__ rows_live) {
   constexpr int G = C / 256;
   const int lane = threadIdx.x & 63;
+  if (rows_live) rows = *rows_live;  // live rows of a capacity-sized grid
   const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
   if (row0 >= rows) return;
   float4 v[R][G];
@@ -106,7 +108,8 @@ __global__ void pack_inputs_kernel(const float* __restrict__ x, const float* __r
                                    const float* __restrict__ mu, const float* __restrict__ spks,
                                    const int32_t* __restrict__ docid,
                                    const int32_t* __restrict__ ext_row, int rows, int mel,
-                                   bf16* __restrict__ a) {
+                                   bf16* __restrict__ a, const int32_t* __restrict__ rows_live) {
+  if (rows_live) rows = *rows_live;
   const int per_row = (4 * mel) / 8;
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (long)rows * per_row) return;
@@ -143,7 +146,9 @@ __global__ void sinusoid_kernel(const float* __restrict__ t, int n_t, int dim,
 }
 
 __global__ void euler_cfg_kernel(float* __restrict__ x, const float* __restrict__ v, int rc,
-                                 int mel, float dt, float cfg) {
+                                 int mel, float dt, float cfg,
+                                 const int32_t* __restrict__ rc_live) {
+  if (rc_live) rc = *rc_live;  // live rows of a capacity-sized grid
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const long n = (long)rc * mel;
   if (i >= n) return;
@@ -183,13 +188,13 @@ inline unsigned blocks_for(long n, int threads) { return (unsigned)((n + threads
 
 hipError_t layer_norm_modulate(const float* h, int C, int rows, const float* mod, long mod_stride,
                                int shift_off, int scale_off, const int32_t* docid, bf16* out,
-                               hipStream_t stream) {
+                               hipStream_t stream, const int32_t* rows_live) {
   if (rows <= 0) return hipSuccess;
   if (C != 1024) return hipErrorInvalidValue;
   constexpr int kRowsPerWave = 1;  // measured best with 1 or 2 (about 5.6 TB/s at 9232 rows)
   hipLaunchKernelGGL((ln_mod_kernel<1024, kRowsPerWave>), dim3(blocks_for(rows, 4 * kRowsPerWave)),
                      dim3(256), 0, stream, h, rows, mod, mod_stride, shift_off, scale_off, docid,
-                     out);
+                     out, rows_live);
   return hipGetLastError();
 }
 
@@ -212,12 +217,12 @@ hipError_t build_aligned_row_index(const int32_t* cu_int, const int32_t* lens,
 
 hipError_t pack_inputs(const float* x, const float* cond, const float* mu, const float* spks,
                        const int32_t* docid, const int32_t* ext_row, int rows, int mel, bf16* a,
-                       hipStream_t stream) {
+                       hipStream_t stream, const int32_t* rows_live) {
   if (rows <= 0) return hipSuccess;
   if (mel % 8 != 0) return hipErrorInvalidValue;
   const long n = (long)rows * (4 * mel / 8);
   hipLaunchKernelGGL(pack_inputs_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, x, cond,
-                     mu, spks, docid, ext_row, rows, mel, a);
+                     mu, spks, docid, ext_row, rows, mel, a, rows_live);
   return hipGetLastError();
 }
 
@@ -228,11 +233,11 @@ hipError_t timestep_sinusoid(const float* t, int n_t, int dim, bf16* out, hipStr
 }
 
 hipError_t euler_cfg_update(float* x, const float* v, int rc, int mel, float dt, float cfg,
-                            hipStream_t stream) {
+                            hipStream_t stream, const int32_t* rc_live) {
   const long n = (long)rc * mel;
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(euler_cfg_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, x, v, rc,
-                     mel, dt, cfg);
+                     mel, dt, cfg, rc_live);
   return hipGetLastError();
 }
 

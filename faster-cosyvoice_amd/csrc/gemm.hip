@@ -59,10 +59,13 @@ struct TileCfg {
   static_assert(TM * WM * 32 == BM && TN * WN * 32 == BN, "wave tiling");
 };
 
-__device__ __forceinline__ void tile_coords(int bid, int total, int tiles_m, int tiles_n,
+// Block bid -> tile (tm, tn) of `total` tiles; false for a block past them (a grid sized for a
+// larger capacity than the live rows need).  Each XCD's blocks take a contiguous tile range.
+__device__ __forceinline__ bool tile_coords(int bid, int total, int tiles_m, int tiles_n,
                                             int group_m, int& tm, int& tn) {
   const int xcd = bid % kXcds, idx = bid / kXcds;
   const int base = total / kXcds, extra = total % kXcds;
+  if (idx >= base + (xcd < extra ? 1 : 0)) return false;
   const int t = xcd * base + min(xcd, extra) + idx;
   const int per_group = group_m * tiles_n;
   const int g = t / per_group;
@@ -71,6 +74,7 @@ __device__ __forceinline__ void tile_coords(int bid, int total, int tiles_m, int
   const int r = t - g * per_group;
   tm = first_m + r % gm;
   tn = r / gm;
+  return true;
 }
 
 // position of 16-byte chunk `chunk` in LDS row `row`: rows of 8 chunks (BK 64) rotate by row/2,
@@ -121,17 +125,18 @@ __device__ __forceinline__ void wait_loads_ahead(int ahead) {
 template <class C, class Epi>
 __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
     const bf16* __restrict__ A, int lda, const bf16* __restrict__ W, int ldw, int M, int N, int K,
-    Epi epi) {
+    Epi epi, const int32_t* __restrict__ m_live) {
   constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN, BK = C::BK, S = C::STAGES;
   // operand ring; after the K loop the same bytes stage the epilogue
   __shared__ __attribute__((aligned(1024))) bf16 smem[S * (BM + BN) * BK];
   bf16 (*sA)[BM * BK] = reinterpret_cast<bf16 (*)[BM * BK]>(smem);
   bf16 (*sB)[BN * BK] = reinterpret_cast<bf16 (*)[BN * BK]>(smem + S * BM * BK);
 
+  if (m_live) M = *m_live;  // live rows of a capacity-sized grid
   const int tiles_n = N / BN;
   const int tiles_m = (M + BM - 1) / BM;
   int tmi, tni;
-  tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, C::kGroupM, tmi, tni);
+  if (!tile_coords(blockIdx.x, tiles_m * tiles_n, tiles_m, tiles_n, C::kGroupM, tmi, tni)) return;
   const int m0 = tmi * BM;
   const int n0 = tni * BN;
   const int lane = threadIdx.x & 63;
@@ -537,7 +542,7 @@ struct EpiGatedResidual {
 struct EpiQkvRope {
   const float* bias;
   int dim;        // heads * 64
-  int rows;       // M (q / k row pitch per head)
+  int rows;       // q / k row pitch per head (rp)
   const int32_t* pos;
   const float* rope_cos;
   const float* rope_sin;
@@ -609,11 +614,11 @@ using Tile32x128 = TileCfg<32, 128, 1, 4>;
 
 template <class C, class Epi>
 hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
-                       const Epi& epi, hipStream_t stream) {
+                       const Epi& epi, hipStream_t stream, const int32_t* m_live) {
   if (N % C::BN != 0 || K % C::BK != 0) return hipErrorInvalidValue;
   const int tiles = ((M + C::BM - 1) / C::BM) * (N / C::BN);
   hipLaunchKernelGGL((gemm_kernel<C, Epi>), dim3(tiles), dim3(C::kThreads), 0, stream, A, lda, W,
-                     ldw, M, N, K, epi);
+                     ldw, M, N, K, epi, m_live);
   return hipGetLastError();
 }
 
@@ -644,21 +649,24 @@ inline int choose_tile(int M, int N) {
   return best;
 }
 
+// M: the rows the grid covers (a capacity when m_live holds the live count, which must not
+// exceed it).  The tile shape is chosen from M; it never changes an element's K summation
+// order, so a layout's results are the same under any capacity.
 template <class Epi>
 hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
-                  const Epi& epi, hipStream_t stream) {
+                  const Epi& epi, hipStream_t stream, const int32_t* m_live = nullptr) {
   if (M <= 0) return hipSuccess;
   if (N % 128 != 0 || K % 64 != 0 || lda % 8 != 0 || ldw % 8 != 0) return hipErrorInvalidValue;
   // the copies address A and W by 32-bit byte offsets from their bases
   if ((long)M * lda * 2 >= (1L << 32) || (long)N * ldw * 2 >= (1L << 32)) return hipErrorInvalidValue;
   switch (choose_tile(M, N)) {
-    case 0: return launch_tile<Tile256x256>(A, lda, W, ldw, M, N, K, epi, stream);
-    case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream);
-    case 2: return launch_tile<Tile128x256>(A, lda, W, ldw, M, N, K, epi, stream);
-    case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream);
-    case 5: return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream);
-    case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream);
-    default: return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream);
+    case 0: return launch_tile<Tile256x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case 2: return launch_tile<Tile128x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case 5: return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    default: return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
   }
 }
 
@@ -666,8 +674,9 @@ hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, 
 
 hipError_t gemm_bias_f32_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                               int M, int N, int K, float* out_f32, bf16* out_bf16, int ldo,
-                              hipStream_t stream) {
-  return launch(A, lda, W, ldw, M, N, K, EpiBiasF32Bf16{bias, out_f32, out_bf16, ldo}, stream);
+                              hipStream_t stream, const int32_t* m_live) {
+  return launch(A, lda, W, ldw, M, N, K, EpiBiasF32Bf16{bias, out_f32, out_bf16, ldo}, stream,
+                m_live);
 }
 
 hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
@@ -684,10 +693,11 @@ hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const f
 
 hipError_t gemm_bias_f32_rowmap(const bf16* A, int lda, const bf16* W, int ldw,
                                 const float* bias, int M, int N, int K, float* out, int ldo,
-                                int n_valid, const int32_t* row_map, hipStream_t stream) {
+                                int n_valid, const int32_t* row_map, hipStream_t stream,
+                                const int32_t* m_live) {
   if (n_valid % 4 != 0) return hipErrorInvalidValue;
   return launch(A, lda, W, ldw, M, N, K, EpiBiasF32RowMap{bias, out, ldo, n_valid, row_map},
-                stream);
+                stream, m_live);
 }
 
 hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
@@ -698,30 +708,33 @@ hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, c
 }
 
 hipError_t gemm_bias_gelu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
-                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream) {
+                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream,
+                               const int32_t* m_live) {
   if ((long)M * ldo * 2 >= (1L << 31)) return hipErrorInvalidValue;  // buffer range is an int
-  return launch(A, lda, W, ldw, M, N, K, EpiBiasGeluBf16{bias, out, ldo}, stream);
+  return launch(A, lda, W, ldw, M, N, K, EpiBiasGeluBf16{bias, out, ldo}, stream, m_live);
 }
 
 hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, float* h, int ldh, const float* gate,
-                               long mod_stride, const int32_t* docid, hipStream_t stream) {
+                               long mod_stride, const int32_t* docid, hipStream_t stream,
+                               const int32_t* m_live) {
   if ((long)M * ldh * 4 >= (1L << 31)) return hipErrorInvalidValue;  // buffer range is an int
   if (mod_stride == 0)
     return launch(A, lda, W, ldw, M, N, K,
-                  EpiGatedResidual<false>{bias, h, ldh, gate, 0, docid}, stream);
+                  EpiGatedResidual<false>{bias, h, ldh, gate, 0, docid}, stream, m_live);
   return launch(A, lda, W, ldw, M, N, K,
-                EpiGatedResidual<true>{bias, h, ldh, gate, mod_stride, docid}, stream);
+                EpiGatedResidual<true>{bias, h, ldh, gate, mod_stride, docid}, stream, m_live);
 }
 
 hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const float* bias, int M,
                          int dim, int heads, const int32_t* pos, const float* rope_cos,
                          const float* rope_sin, int rope_dim, int max_pos, bf16* q, bf16* k,
-                         bf16* vt, int rp, hipStream_t stream) {
+                         bf16* vt, int rp, hipStream_t stream, const int32_t* m_live) {
   (void)heads;
+  if (rp < M) return hipErrorInvalidValue;
   return launch(A, lda, W, ldw, M, 3 * dim, dim,
-                EpiQkvRope{bias, dim, M, pos, rope_cos, rope_sin, rope_dim, max_pos, q, k, vt, rp},
-                stream);
+                EpiQkvRope{bias, dim, rp, pos, rope_cos, rope_sin, rope_dim, max_pos, q, k, vt, rp},
+                stream, m_live);
 }
 
 }  // namespace fcv

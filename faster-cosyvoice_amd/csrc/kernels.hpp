@@ -9,13 +9,22 @@
 
 namespace fcv {
 
+// ---- live counts -------------------------------------------------------------------------
+// A planned layout's counts as the kernels read them from device memory (int32[4] in the
+// workspace): the grids are sized for the plan's capacity and the workgroups past the live
+// count exit at once, so a graph captured for a capacity replays for any layout that fits it.
+// Launchers given live == nullptr use their static count arguments.
+enum { kLiveRows = 0, kLiveTiles = 1, kLiveHalfRows = 2 };  // internal rows, attention tiles, rc
+
 // ---- GEMM: C[M,N] = A[M,K] . W[N,K]^T (+ bias) with a fused epilogue -------------------
 // Requirements checked by the caller: N % 128 == 0, K % 64 == 0, lda/ldw % 8 == 0.
+// M is the capacity the grid is sized for; m_live (when not null) holds the live row count
+// (<= M).
 
 // out_f32[r, c] = acc + bias[c];  out_bf16[r, c] = bf16(same)   (input projection)
 hipError_t gemm_bias_f32_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                               int M, int N, int K, float* out_f32, bf16* out_bf16, int ldo,
-                              hipStream_t stream);
+                              hipStream_t stream, const int32_t* m_live = nullptr);
 
 // out[r, c] = acc + bias[c] for c < n_valid (fp32; AdaLN projection)
 hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
@@ -24,7 +33,8 @@ hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const f
 // out[row_map[r], c] = acc + bias[c] for c < n_valid and row_map[r] >= 0 (proj_out)
 hipError_t gemm_bias_f32_rowmap(const bf16* A, int lda, const bf16* W, int ldw,
                                 const float* bias, int M, int N, int K, float* out, int ldo,
-                                int n_valid, const int32_t* row_map, hipStream_t stream);
+                                int n_valid, const int32_t* row_map, hipStream_t stream,
+                                const int32_t* m_live = nullptr);
 
 // out[r, c] = bf16(silu(acc + bias[c]))   (timestep MLP)
 hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
@@ -32,21 +42,23 @@ hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, c
 
 // out[r, c] = bf16(gelu_tanh(acc + bias[c]))   (FF1)
 hipError_t gemm_bias_gelu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
-                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream);
+                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream,
+                               const int32_t* m_live = nullptr);
 
 // h[r, c] += gate[c] * (acc + bias[c]), gate row = mod + docid[r] * mod_stride + gate_off
 // (out-projection and FF2 gated residuals)
 hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, float* h, int ldh, const float* mod,
-                               long mod_stride, const int32_t* docid, hipStream_t stream);
+                               long mod_stride, const int32_t* docid, hipStream_t stream,
+                               const int32_t* m_live = nullptr);
 
 // Fused QKV projection: bias, interleaved RoPE on columns [0, rope_dim) of q and k
 // (angles from cos/sin tables [max_pos][rope_dim/2], row position min(pos[r], max_pos-1)),
-// scatter to q, k : [heads][M][dim_head] and vt : [heads][dim_head][rp] (V transposed).
+// scatter to q, k : [heads][rp][dim_head] and vt : [heads][dim_head][rp] (V transposed).
 hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const float* bias, int M,
                          int dim, int heads, const int32_t* pos, const float* rope_cos,
                          const float* rope_sin, int rope_dim, int max_pos, bf16* q, bf16* k,
-                         bf16* vt, int rp, hipStream_t stream);
+                         bf16* vt, int rp, hipStream_t stream, const int32_t* m_live = nullptr);
 
 // ---- skinny products (few rows sharing W, K in {512, 1024}): bandwidth-bound, no MFMA -------
 // Launches of up to 16 rows each; a row's result is the same whatever M is.
@@ -60,13 +72,14 @@ hipError_t gemv_bias_silu_bf16(const bf16* a, int lda, const bf16* W, int ldw, c
 
 // ---- attention ----------------------------------------------------------------------------
 // Varlen attention, head_dim 64.  Document d starts at row doc_start[d] (a multiple of 8)
-// and has doc_len[d] real rows; tiles[i] = {doc, first query row}.
-// chunk == 0: full attention inside each document; chunk > 0: key visible iff
-// (key_pos / chunk) <= (query_pos / chunk).
+// and has doc_len[d] real rows; tiles[i] = {doc, first query row}.  q, k: [heads][rp][64],
+// vt: [heads][64][rp].  chunk == 0: full attention inside each document; chunk > 0: key
+// visible iff (key_pos / chunk) <= (query_pos / chunk).  n_tiles is the grid's capacity;
+// tiles_live (when not null) holds the live tile count.
 hipError_t attention_varlen(const bf16* q, const bf16* k, const bf16* vt, bf16* o,
                             const int32_t* doc_start, const int32_t* doc_len,
-                            const int32_t* tiles, int n_tiles, int rows, int rp, int heads,
-                            int chunk, hipStream_t stream);
+                            const int32_t* tiles, int n_tiles, int rp, int heads, int chunk,
+                            hipStream_t stream, const int32_t* tiles_live = nullptr);
 constexpr int kAttnTileQ = 128;
 
 // ---- causal grouped conv position embedding (64 channels per group) -------------------------
@@ -74,13 +87,13 @@ constexpr int kAttnTileQ = 128;
 // the row's document start read as zero.  out_bf16 != null: store y;  h != null: h += y.
 hipError_t conv_causal_mish(const bf16* x, int C, const bf16* w, const float* bias, int taps,
                             const int32_t* pos, int rows, bf16* out_bf16, float* h,
-                            hipStream_t stream);
+                            hipStream_t stream, const int32_t* rows_live = nullptr);
 
 // ---- bandwidth-bound kernels -----------------------------------------------------------------
 // out[r, :] = bf16(LN(h[r, :]) * scale + shift), scale/shift rows = mod + docid[r]*mod_stride + off
 hipError_t layer_norm_modulate(const float* h, int C, int rows, const float* mod, long mod_stride,
                                int shift_off, int scale_off, const int32_t* docid, bf16* out,
-                               hipStream_t stream);
+                               hipStream_t stream, const int32_t* rows_live = nullptr);
 
 // docid[r], pos[r] from device cu_seqlens[n_docs+1].
 hipError_t build_row_index(const int32_t* cu_seqlens, int n_docs, int rows, int32_t* docid,
@@ -96,14 +109,15 @@ hipError_t build_aligned_row_index(const int32_t* cu_int, const int32_t* lens,
 // a[r, 0:4*mel] = bf16([x[e], cond[e], mu[e], spks[docid[r]]]) with e = ext_row[r]; zeros when e < 0
 hipError_t pack_inputs(const float* x, const float* cond, const float* mu, const float* spks,
                        const int32_t* docid, const int32_t* ext_row, int rows, int mel, bf16* a,
-                       hipStream_t stream);
+                       hipStream_t stream, const int32_t* rows_live = nullptr);
 
 // out[m, 0:dim] = bf16([sin(1000 t_m f), cos(1000 t_m f)]), f_i = exp(-i ln(1e4)/(dim/2-1))
 hipError_t timestep_sinusoid(const float* t, int n_t, int dim, bf16* out, hipStream_t stream);
 
 // x[r] += dt * ((1+cfg) v[r] - cfg v[r+rc]); x[r+rc] = x[r]   for r < rc
+// (rc = rc_live[0] when rc_live is not null; the grid covers the capacity rc)
 hipError_t euler_cfg_update(float* x, const float* v, int rc, int mel, float dt, float cfg,
-                            hipStream_t stream);
+                            hipStream_t stream, const int32_t* rc_live = nullptr);
 
 // [B, C, T] channel-first padded <-> packed rows [R, C]
 hipError_t pack_padded(const float* src, int batch, int channels, int padded_len,

@@ -100,16 +100,25 @@ class _PackedRunner:
             raise RuntimeError("call finalize_weights() before running the estimator")
         return self._handle
 
-    def plan(self, seqlens: Sequence[int], streaming: bool = False) -> None:
-        """Plan the packed layout (FlashInfer ``plan`` equivalent); no-op when unchanged."""
+    def plan(self, seqlens: Sequence[int], streaming: bool = False,
+             capacity: tuple[int, int] | None = None) -> None:
+        """Plan the packed layout (FlashInfer ``plan`` equivalent); no-op when unchanged.
+
+        ``capacity = (rows_cap, docs_cap)`` plans the layout inside that capacity
+        (``fcv_dit_plan_capacity``): every layout planned into one capacity shares the solve
+        graphs captured for it; None plans exactly this layout."""
         handle = self._require()
         lengths = tuple(int(n) for n in seqlens)
-        key = (lengths, bool(streaming))
+        key = (lengths, bool(streaming), capacity)
         if key == self._plan_key:
             return
         lib = _lib.load()
         rows = sum(lengths)
-        need = lib.fcv_dit_workspace_bytes(handle, rows, len(lengths))
+        rows_cap, docs_cap = capacity if capacity is not None else (rows, len(lengths))
+        if rows > rows_cap or len(lengths) > docs_cap:
+            raise ValueError(f"{rows} rows in {len(lengths)} documents exceed the capacity "
+                             f"({rows_cap}, {docs_cap})")
+        need = lib.fcv_dit_workspace_bytes(handle, rows_cap, docs_cap)
         if self._workspace is None or self._workspace.numel() < need:
             cap = max(need, 2 * (0 if self._workspace is None else self._workspace.numel()))
             self._workspace = None
@@ -121,11 +130,18 @@ class _PackedRunner:
             cu.append(cu[-1] + n)
         cu_arr = (_lib.c_int32 * len(cu))(*cu)
         mode = _lib.FCV_MASK_CHUNK_CAUSAL if streaming else _lib.FCV_MASK_FULL
-        _lib.check(lib.fcv_dit_plan(handle, cu_arr, len(lengths), mode, self.static_chunk_size,
-                                    aligned, self._workspace.numel() - (aligned - base),
-                                    self._stream_ptr()))
+        _lib.check(lib.fcv_dit_plan_capacity(handle, cu_arr, len(lengths), mode,
+                                             self.static_chunk_size, rows_cap, docs_cap, aligned,
+                                             self._workspace.numel() - (aligned - base),
+                                             self._stream_ptr()))
         self._plan_key = key
         self.plan_calls += 1
+
+    def graph_stats(self) -> tuple[int, int]:
+        """(solve graphs held, solves captured so far) of this runner's handle."""
+        pooled, captures = _lib.c_int32(), _lib.c_int32()
+        _lib.check(_lib.load().fcv_dit_graph_stats(self._require(), pooled, captures))
+        return pooled.value, captures.value
 
     def _stream_ptr(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream

@@ -2,11 +2,15 @@
 
 ``solve_euler_packed`` keeps the sample packed and fp32 across steps and runs the whole
 n-step loop inside libfcvdit (``fcv_dit_solve``).  With ``use_graph`` the loop is replayed from
-a hipGraph once the same layout and buffers come back: a layout's first solve runs eagerly and
-its second captures the graph, since a capture costs more than one eager run (a streaming
-step, whose layout is new every call, never captures).
+a hipGraph once the same capacity and buffers come back: a capacity's first solve runs eagerly
+and its second captures the graph, since a capture costs more than one eager run.
 ``solve_euler_batched`` keeps the reference's padded signature for callers that hand it
 ``[B,80,T]`` tensors and a padding mask.
+
+By default a solve plans its layout into a capacity bucket (``capacity_bucket``): the
+kernels read the layout from device memory, so the graph captured for a bucket replays for
+every later layout that fits it (a streaming step or a new batch composition), where an exact
+plan's graph serves only that layout.  Results are bit-identical either way.
 """
 
 from __future__ import annotations
@@ -39,15 +43,43 @@ def euler_schedule(n_steps: int) -> tuple[list[float], list[float]]:
     return ts, dts
 
 
-def _solver_buffers(runner: _PackedRunner, dims, rc: int, n_req: int) -> dict[str, torch.Tensor]:
-    """Packed CFG input buffers [2*rc, 80] (zero second halves) reused while the shape holds."""
-    key = (rc, n_req)
-    bufs = getattr(runner, "_solver_bufs", None)
-    if bufs is None or bufs["key"] != key:
+def capacity_bucket(rows: int, n_docs: int) -> tuple[int, int]:
+    """The capacity a packed CFG layout of ``rows`` rows in ``n_docs`` documents is planned
+    into: rows rounded up to m * 2^e with m in 8..15 (at most 12.5 % above, at least 256),
+    documents to a power of two.  Any two layouts in one bucket share its solve graphs."""
+    cap = 256
+    while cap < rows:
+        cap *= 2
+    # cap is the smallest power of two >= rows; the eighths of the power below refine it
+    low = cap // 2
+    for m in range(9, 17):
+        if m * low // 8 >= rows:
+            cap = max(256, m * low // 8)
+            break
+    docs = 2
+    while docs < n_docs:
+        docs *= 2
+    return cap, docs
+
+
+_BUFFER_SETS = 4  # solver buffer sets kept per runner: one per graph its handle can pool
+
+
+def _solver_buffers(runner: _PackedRunner, dims, rows_cap: int,
+                    docs_cap: int) -> dict[str, torch.Tensor]:
+    """Packed CFG input buffers for up to ``rows_cap`` rows in ``docs_cap`` documents.  A set
+    per capacity is kept (the most recently used few), so the buffer pointers a captured graph
+    was recorded with come back with its capacity and the graph can be replayed."""
+    key = (rows_cap, docs_cap)
+    sets = runner.__dict__.setdefault("_solver_bufs", {})
+    bufs = sets.pop(key, None)
+    if bufs is None:
         mel, dev = dims.mel_dim, runner.device
         z = lambda rows: torch.zeros(rows, mel, dtype=torch.float32, device=dev)
-        bufs = {"key": key, "x": z(2 * rc), "mu": z(2 * rc), "cond": z(2 * rc), "spks": z(2 * n_req)}
-        runner._solver_bufs = bufs
+        bufs = {"x": z(rows_cap), "mu": z(rows_cap), "cond": z(rows_cap), "spks": z(docs_cap)}
+        while len(sets) >= _BUFFER_SETS:
+            sets.pop(next(iter(sets)))  # least recently used
+    sets[key] = bufs  # most recently used last
     return bufs
 
 
@@ -79,18 +111,23 @@ def request_groups(lengths: Sequence[int], n_groups: int) -> list[list[int]]:
 def _solve_on(runner: _PackedRunner, dims, noise: torch.Tensor, mu: torch.Tensor,
               cond: torch.Tensor, spks: torch.Tensor, lengths: list[int], t_arr, dt_arr,
               n_steps: int, cfg_rate: float, streaming: bool, use_graph: bool,
-              stream: torch.cuda.Stream) -> torch.Tensor:
+              stream: torch.cuda.Stream, bucketed: bool) -> torch.Tensor:
     """One packed CFG solve on ``runner``, enqueued on ``stream`` (the caller orders it)."""
-    rc = sum(lengths)
+    rc, b = sum(lengths), len(lengths)
+    capacity = capacity_bucket(2 * rc, 2 * b) if bucketed else None
     with torch.cuda.stream(stream):
-        runner.plan(lengths + lengths, streaming)
-        # persistent solver buffers: stable pointers let a captured graph be replayed
-        buf = _solver_buffers(runner, dims, rc, len(lengths))
+        runner.plan(lengths + lengths, streaming, capacity)
+        # persistent solver buffers: stable pointers let a captured graph be replayed; the
+        # unconditional half [rc, 2 rc) of mu and cond and spks[b:2b] must read zero
+        buf = _solver_buffers(runner, dims, *(capacity or (2 * rc, 2 * b)))
         buf["x"][:rc].copy_(noise)
-        buf["x"][rc:].copy_(noise)
+        buf["x"][rc:2 * rc].copy_(noise)
         buf["mu"][:rc].copy_(mu)
+        buf["mu"][rc:2 * rc].zero_()
         buf["cond"][:rc].copy_(cond)
-        buf["spks"][: len(lengths)].copy_(spks)
+        buf["cond"][rc:2 * rc].zero_()
+        buf["spks"][:b].copy_(spks)
+        buf["spks"][b:2 * b].zero_()
         _lib.check(_lib.load().fcv_dit_solve(
             runner._require(), buf["x"].data_ptr(), buf["mu"].data_ptr(),
             buf["cond"].data_ptr(), buf["spks"].data_ptr(), t_arr, dt_arr, n_steps,
@@ -101,7 +138,8 @@ def _solve_on(runner: _PackedRunner, dims, noise: torch.Tensor, mu: torch.Tensor
 def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.Tensor,
                        cond: torch.Tensor, spks: torch.Tensor, lengths: Sequence[int],
                        n_steps: int = 10, cfg_rate: float = 0.7, streaming: bool = False,
-                       use_graph: bool = True, concurrency: int | None = None) -> torch.Tensor:
+                       use_graph: bool = True, concurrency: int | None = None,
+                       bucketed: bool = True) -> torch.Tensor:
     """CFG Euler solve on packed request rows.
 
     noise, mu, cond: ``[Rc, 80]`` conditional rows of the B requests (doc-major);
@@ -114,6 +152,9 @@ def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.T
     before any is waited for.  One group's tail rounds and bandwidth-bound phases then overlap
     the other's matrix work.  A document's result does not depend on what it is packed with,
     so the rows are bit-identical to one packed batch of all requests.
+
+    ``bucketed`` plans each group into its capacity bucket (``capacity_bucket``), so a new
+    layout in a bucket that has been captured replays its graph; False plans the exact layout.
     """
     lengths = [int(n) for n in lengths]
     rc = sum(lengths)
@@ -137,7 +178,7 @@ def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.T
         stream = _stream_for(estimator)
         stream.wait_stream(current)
         result = _solve_on(estimator, estimator.dims, noise, mu, cond, spks, lengths, t_arr,
-                           dt_arr, n_steps, cfg_rate, streaming, use_graph, stream)
+                           dt_arr, n_steps, cfg_rate, streaming, use_graph, stream, bucketed)
         current.wait_stream(stream)
         return result
     offs = [0]
@@ -154,7 +195,7 @@ def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.T
         with torch.cuda.stream(stream):
             out = _solve_on(runner, estimator.dims, noise[rows], mu[rows], cond[rows], spks[g],
                             [lengths[i] for i in g], t_arr, dt_arr, n_steps, cfg_rate,
-                            streaming, use_graph, stream)
+                            streaming, use_graph, stream, bucketed)
             rows.record_stream(stream)
         parts.append((rows, out))
     for s in streams:

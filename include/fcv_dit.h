@@ -76,9 +76,10 @@ const char* fcv_last_error(void);
 int fcv_dit_create(const FcvDitDims* dims, const FcvDitWeights* weights, FcvDit** out);
 int fcv_dit_destroy(FcvDit* dit);
 
-/* Device workspace needed for a packed batch of `rows` rows and `n_docs` documents
- * (replaces the reference's 64 MB FlashInfer workspace, flashinfer_attention.py:13,55,
- * and the activations torch allocates per forward). Monotone in both arguments. */
+/* Device workspace needed for a packed batch of `rows` rows and `n_docs` documents, or for a
+ * capacity of that many (fcv_dit_plan_capacity) (replaces the reference's 64 MB FlashInfer
+ * workspace, flashinfer_attention.py:13,55, and the activations torch allocates per forward).
+ * Monotone in both arguments. */
 size_t fcv_dit_workspace_bytes(const FcvDit* dit, int32_t rows, int32_t n_docs);
 
 /* Plan a packed layout (replaces RaggedAttentionRunner._prepare / wrapper.plan,
@@ -88,9 +89,22 @@ size_t fcv_dit_workspace_bytes(const FcvDit* dit, int32_t rows, int32_t n_docs);
  * below 2 GB (the kernels address activations by 32-bit byte offsets; about 5 x 10^5 rows at
  * the Token2Wav dims).  mask_mode: FCV_MASK_FULL or FCV_MASK_CHUNK_CAUSAL
  * (key k visible to query q iff k/chunk <= q/chunk, flashinfer_attention.py:16-33).
- * The workspace is bound to the handle until the next plan.  Synchronous on `stream`. */
+ * The workspace is bound to the handle until the next plan.  Synchronous on `stream`.
+ * Same as fcv_dit_plan_capacity with a capacity of exactly this layout's rows and documents. */
 int fcv_dit_plan(FcvDit* dit, const int32_t* cu_seqlens_host, int32_t n_docs, int32_t mask_mode,
                  int32_t chunk, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Plan a layout inside a capacity of rows_cap caller rows in docs_cap documents (the layout
+ * must fit: rows <= rows_cap, n_docs <= docs_cap).  The replacement of the reference's bucketed
+ * graph runners (flashinfer_dit.py:742-804: one captured graph per padded length, a runtime
+ * padding boundary) for the packed layout: the workspace layout and every kernel grid depend on
+ * the capacity only, and the kernels read the layout's live row, tile and document tables from
+ * the workspace, so a solve graph captured under one layout replays for any other layout
+ * planned into the same capacity (and workspace), with results bit-identical to an exact plan.
+ * Workspace: fcv_dit_workspace_bytes(dit, rows_cap, docs_cap). */
+int fcv_dit_plan_capacity(FcvDit* dit, const int32_t* cu_seqlens_host, int32_t n_docs,
+                          int32_t mask_mode, int32_t chunk, int32_t rows_cap, int32_t docs_cap,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* One estimator forward over the planned packed batch (FlashInferDiT._forward_packed,
  * flashinfer_dit.py:447-543).  x, mu, cond: [rows][mel]; spks: [n_docs][mel];
@@ -109,11 +123,12 @@ int fcv_euler_cfg_step(FcvDit* dit, float* x, const float* v, float dt, float cf
  * batch: n_steps x (forward with t_host[step] shared by all documents, then the CFG Euler
  * update with dt_host[step]).  x: [rows][mel], both halves equal on entry, updated in place.
  * mu/cond/spks as in fcv_dit_forward (zeros in the unconditional half).  use_graph != 0
- * replays a hipGraph of the whole loop when the plan, the pointers and the schedule (dt_host,
- * cfg, n_steps) match the cached graph's; a solve with a new key runs eagerly, and the next
- * solve with that same key captures it (a capture costs more than one eager run, so a layout
- * used once, as in streaming, is never captured).  Results are identical either way.
- * n_steps <= 64. */
+ * replays a hipGraph of the whole loop when the plan's capacity and mask, the workspace and the
+ * pointers and the schedule (dt_host, cfg, n_steps) match a captured graph's; the handle keeps
+ * the 4 most recently used graphs (the reference pools 4 plans, flashinfer_dit.py:143,192-226).
+ * A solve with a new key runs eagerly, and the next solve with that same key captures it (a
+ * capture costs more than one eager run, so a key used once is never captured).  Layouts
+ * planned into one capacity share a key.  Results are identical either way.  n_steps <= 64. */
 int fcv_dit_solve(FcvDit* dit, float* x, const float* mu, const float* cond, const float* spks,
                   const float* t_host, const float* dt_host, int32_t n_steps, float cfg,
                   int32_t use_graph, hipStream_t stream);
@@ -125,6 +140,11 @@ int fcv_pack_padded(FcvDit* dit, const float* src, int32_t batch, int32_t channe
                     int32_t padded_len, float* dst, hipStream_t stream);
 int fcv_unpack_padded(FcvDit* dit, const float* src, int32_t batch, int32_t channels,
                       int32_t padded_len, float* dst, hipStream_t stream);
+
+/* Solve graphs the handle holds (at most 4) and how many solves it has captured so far: a
+ * layout planned into a captured capacity replays without a new capture.  No counterpart in the
+ * reference beyond its plan_calls counter (flashinfer_attention.py:61-62). */
+int fcv_dit_graph_stats(const FcvDit* dit, int32_t* pooled, int32_t* captures);
 
 /* Planned layout facts (for callers sizing buffers): rows, documents, attention tiles. */
 int fcv_dit_plan_info(const FcvDit* dit, int32_t* rows, int32_t* n_docs, int32_t* n_tiles);
