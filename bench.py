@@ -204,15 +204,27 @@ def hift_leg(fcv, batch, dev, cpu: bool) -> dict:
     g = torch.Generator().manual_seed(6)
     mels = [torch.randn(80, n, generator=g).to(dev) for n in gen]
     voc.inference_batched(mels)
+    voc.inference_batched(mels)  # each group's capacity graph is captured here
     stream = torch.cuda.current_stream(dev)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    for _ in range(HIFT_REPEAT):
-        voc.inference_batched(mels)
-    stop.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / HIFT_REPEAT
+
+    def timed(graph: bool, ms_in=mels, fin=None, repeat=HIFT_REPEAT) -> float:
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(repeat):
+            voc.inference_batched(ms_in, fin, graph=graph)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / repeat
+
+    ms = timed(True)
+    ms_eager = timed(False)
+    # one streaming chunk: 60 new Mel frames after 8 frames of right context, not final
+    chunk = [torch.randn(80, 68, generator=g).to(dev)]
+    voc.inference_batched(chunk, [False])
+    voc.inference_batched(chunk, [False])
+    chunk_ms = timed(True, chunk, [False], 20)
+    chunk_eager = timed(False, chunk, [False], 20)
     frames = sum(gen)
     audio_s = frames * dims.upsample_scale / dims.sampling_rate
     macs = fcv.synthetic.hift_macs_per_frame(dims)
@@ -223,12 +235,17 @@ def hift_leg(fcv, batch, dev, cpu: bool) -> dict:
                 "request groups (fp32, F0 predictor fp64)",
         "requests": len(gen), "mel_frames": frames, "audio_seconds": round(audio_s, 2),
         "ms_per_call": round(ms, 3),
+        "eager_ms_per_call": round(ms_eager, 3),
+        "stream_chunk": {"what": "one non-final request of 68 Mel frames (60 new + 8 right "
+                                 "context), 20 calls", "ms_per_call": round(chunk_ms, 4),
+                         "eager_ms_per_call": round(chunk_eager, 4)},
         "audio_seconds_per_second": round(audio_s / (ms * 1e-3), 1),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_TFLOPS, 4),
                      "flop_per_frame": 2 * sum(v for k, v in macs.items() if k != "f0_fp64"),
-                     "timing": f"HIP events around {HIFT_REPEAT} back-to-back calls; achieved "
-                               "counts the fp32 convolutions of the whole call"},
+                     "timing": f"HIP events around {HIFT_REPEAT} back-to-back calls replayed from "
+                               "the groups' capacity graphs; achieved counts the fp32 "
+                               "convolutions of the whole call"},
     }
     if cpu:
         from oracle import hift_oracle as HO

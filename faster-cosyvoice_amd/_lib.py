@@ -114,6 +114,12 @@ SIGNATURES = {
     "fcv_hift_inference": (c_int32, [c_void_p, c_void_p, POINTER(c_int32), POINTER(c_int32),
                                      c_int32, c_void_p, c_void_p, c_void_p, c_size_t,
                                      c_void_p]),
+    "fcv_hift_workspace_bytes_capacity": (c_size_t, [c_void_p, c_int32, c_int32]),
+    "fcv_hift_inference_capacity": (c_int32, [c_void_p, c_void_p, POINTER(c_int32),
+                                              POINTER(c_int32), c_int32, c_int32, c_int32,
+                                              c_void_p, c_void_p, c_void_p, c_size_t, c_int32,
+                                              c_void_p]),
+    "fcv_hift_graph_stats": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32)]),
 }
 
 STAGES = ("qkv", "attention", "out_proj", "ff1", "ff2", "ln_mod", "conv", "adaln", "in_proj",

@@ -84,7 +84,8 @@ __device__ void conv_store(const HiftConv& p, long row, int cb, int lg,
 // BK input channels of one tap per chunk (cin_pad % BK == 0); each loader thread moves BK / 16
 // groups of 4 elements per operand, each lane feeds k = 16 m + 4 lg + s at MFMA step (m, s)
 template <typename T, int BK>
-__global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const HiftDocs docs) {
+__global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p,
+                                                        const HiftDocs* __restrict__ docs) {
   using VT = typename Vec4<T>::type;
   constexpr int PITCH = BK + 4;  // LDS row pitch in elements (conflict-free 16-byte reads)
   constexpr int G = BK / 16;
@@ -96,7 +97,10 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const 
   const int wave = tid >> 6;
   const int wc = wave & 1, wt = wave >> 1;
   const int li = lane & 15, lg = lane >> 4;
+  const int n_docs = docs->n;
+  const int rows_out = docs->b[n_docs];  // live rows (the grid covers the capacity)
   const int r0 = blockIdx.x * kTileR;
+  if (r0 >= rows_out) return;
   const int co0 = blockIdx.y * kTileC;
   const int cpt = p.cin_pad / BK;
   const int KC = p.k * cpt;
@@ -105,13 +109,13 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const 
   // loader roles: weight row lr / input row lr, 4-element quarter lq of the 16-channel chunk
   const int lr = tid >> 2, lq = tid & 3;
   const int r = r0 + lr;
-  const bool valid = r < p.rows_out;
+  const bool valid = r < rows_out;
   int in_base = 0, in_len = 0, pos = 0;
   if (valid) {
-    const int d = doc_of(docs.b, p.n_docs, r);
-    pos = r - docs.b[d];
-    in_base = docs.a[d];
-    in_len = docs.a[d + 1] - in_base;
+    const int d = doc_of(docs->b, n_docs, r);
+    pos = r - docs->b[d];
+    in_base = docs->a[d];
+    in_len = docs->a[d + 1] - in_base;
   }
   const T* X = static_cast<const T*>(p.x);
   const T* W = static_cast<const T*>(p.w) + (long)(co0 + lr) * kcin + 4 * lq;
@@ -203,24 +207,26 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p, const 
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
     const int rr = r0 + wt * 32 + b * 16 + li;
-    if (rr >= p.rows_out) continue;
-    const int d = doc_of(docs.b, p.n_docs, rr);
-    const int pp = rr - docs.b[d];
-    const long row_w = p.reflect ? (long)docs.b[d] + d + 1 + pp : rr;
+    if (rr >= rows_out) continue;
+    const int d = doc_of(docs->b, n_docs, rr);
+    const int pp = rr - docs->b[d];
+    const long row_w = p.reflect ? (long)docs->b[d] + d + 1 + pp : rr;
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
       const int cb = co0 + wc * 32 + a * 16;
       conv_store<T>(p, row_w, cb, lg, acc[a][b]);
       // reflection padding (1, 0): row 0 of the document repeats the result's row 1
-      if (p.reflect && pp == 1) conv_store<T>(p, (long)docs.b[d] + d, cb, lg, acc[a][b]);
+      if (p.reflect && pp == 1) conv_store<T>(p, (long)docs->b[d] + d, cb, lg, acc[a][b]);
     }
   }
 }
 
 __global__ __launch_bounds__(256) void snake_kernel(const float* __restrict__ x, int ldx,
-                                                    float* __restrict__ out, int ldo, int rows,
-                                                    int C, const float* __restrict__ alpha,
-                                                    const float* __restrict__ inv_alpha) {
+                                                    float* __restrict__ out, int ldo, int C,
+                                                    const float* __restrict__ alpha,
+                                                    const float* __restrict__ inv_alpha,
+                                                    const HiftDocs* __restrict__ docs) {
+  const int rows = docs->b[docs->n];
   const int q = C / 4;
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (long)rows * q) return;
@@ -234,7 +240,9 @@ __global__ __launch_bounds__(256) void snake_kernel(const float* __restrict__ x,
 }
 
 __global__ __launch_bounds__(256) void to_f64_kernel(const float* __restrict__ x,
-                                                     double* __restrict__ y, long n) {
+                                                     double* __restrict__ y, int C,
+                                                     const HiftDocs* __restrict__ docs) {
+  const long n = (long)docs->a[docs->n] * C;
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = (double)x[i];
 }
@@ -242,8 +250,10 @@ __global__ __launch_bounds__(256) void to_f64_kernel(const float* __restrict__ x
 __global__ __launch_bounds__(64) void f0_head_kernel(const double* __restrict__ h, int C,
                                                      const double* __restrict__ w,
                                                      const double* __restrict__ b,
-                                                     float* __restrict__ f0) {
+                                                     float* __restrict__ f0,
+                                                     const HiftDocs* __restrict__ docs) {
   const long r = blockIdx.x;
+  if (r >= docs->b[docs->n]) return;
   double s = 0.0;
   for (int c = threadIdx.x; c < C; c += 64) s = fma(h[r * C + c], w[c], s);
 #pragma unroll
@@ -260,13 +270,13 @@ __global__ __launch_bounds__(64) void f0_head_kernel(const double* __restrict__ 
 // CPU, whose kernel accumulates fp32 in double: an fp32 running sum drifts by ~1e-6 relative
 // per few hundred frames, and the phase multiplies that by 2 pi x 480.
 __global__ __launch_bounds__(64) void source_phase_kernel(const HiftSource p,
-                                                          const HiftDocs docs) {
+                                                          const HiftDocs* __restrict__ docs) {
 #pragma clang fp contract(off)
   const int d = blockIdx.x;
   const int h = threadIdx.x;
-  if (h >= p.H) return;
-  const int f_base = docs.a[d];
-  const int T = docs.a[d + 1] - f_base;
+  if (h >= p.H || d >= docs->n) return;
+  const int f_base = docs->a[d];
+  const int T = docs->a[d + 1] - f_base;
   const long L = (long)T * p.scale;
   const float mult = (float)(h + 1);
   const float sr = (float)p.sampling_rate;
@@ -295,13 +305,13 @@ __global__ __launch_bounds__(64) void source_phase_kernel(const HiftSource p,
 }
 
 __global__ __launch_bounds__(256) void source_sample_kernel(const HiftSource p,
-                                                            const HiftDocs docs, int samples) {
+                                                            const HiftDocs* __restrict__ docs) {
 #pragma clang fp contract(off)
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= samples) return;
-  const int d = doc_of(docs.b, p.n_docs, n);
-  const int pos = n - docs.b[d];
-  const int fr = docs.a[d] + pos / p.scale;
+  if (n >= docs->b[docs->n]) return;
+  const int d = doc_of(docs->b, docs->n, n);
+  const int pos = n - docs->b[d];
+  const int fr = docs->a[d] + pos / p.scale;
   const float f0 = p.f0[fr];
   const float uv = f0 > p.voiced_threshold ? 1.0f : 0.0f;
   const float amp = uv * p.noise_std + ((1.0f - uv) * p.sine_amp) / 3.0f;
@@ -320,14 +330,14 @@ __device__ __forceinline__ float sin16(int m) { return sinpif((float)(m & 15) / 
 
 __global__ __launch_bounds__(256) void stft_kernel(const float* __restrict__ s,
                                                    const float* __restrict__ win,
-                                                   float* __restrict__ out, int ld, int n_docs,
-                                                   int frames, const HiftDocs docs) {
+                                                   float* __restrict__ out, int ld,
+                                                   const HiftDocs* __restrict__ docs) {
   const int f = blockIdx.x * blockDim.x + threadIdx.x;
-  if (f >= frames) return;
-  const int d = doc_of(docs.b, n_docs, f);
-  const int fl = f - docs.b[d];
-  const float* x = s + docs.a[d];
-  const int L = docs.a[d + 1] - docs.a[d];
+  if (f >= docs->b[docs->n]) return;
+  const int d = doc_of(docs->b, docs->n, f);
+  const int fl = f - docs->b[d];
+  const float* x = s + docs->a[d];
+  const int L = docs->a[d + 1] - docs->a[d];
   float v[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
@@ -354,9 +364,10 @@ __global__ __launch_bounds__(256) void stft_kernel(const float* __restrict__ s,
 // windowed inverse real DFT of one frame: mag = min(exp(y[k]), 100), ph = sin(y[9 + k])
 __global__ __launch_bounds__(256) void istft_frame_kernel(const float* __restrict__ y, int ldy,
                                                           const float* __restrict__ win,
-                                                          float* __restrict__ fr, int frames) {
+                                                          float* __restrict__ fr,
+                                                          const HiftDocs* __restrict__ docs) {
   const int f = blockIdx.x * blockDim.x + threadIdx.x;
-  if (f >= frames) return;
+  if (f >= docs->a[docs->n]) return;
   const float* row = y + (long)f * ldy;
   float re[9], im[9];
 #pragma unroll
@@ -382,14 +393,13 @@ __global__ __launch_bounds__(256) void istft_frame_kernel(const float* __restric
 __global__ __launch_bounds__(256) void istft_ola_kernel(const float* __restrict__ fr,
                                                         const float* __restrict__ win,
                                                         float* __restrict__ out, float limit,
-                                                        int n_docs, int samples,
-                                                        const HiftDocs docs) {
+                                                        const HiftDocs* __restrict__ docs) {
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= samples) return;
-  const int d = doc_of(docs.b, n_docs, n);
-  const int P = n - docs.b[d] + 8;
-  const int f_base = docs.a[d];
-  const int F = docs.a[d + 1] - f_base;
+  if (n >= docs->b[docs->n]) return;
+  const int d = doc_of(docs->b, docs->n, n);
+  const int P = n - docs->b[d] + 8;
+  const int f_base = docs->a[d];
+  const int F = docs->a[d + 1] - f_base;
   float y = 0.0f, env = 0.0f;
   const int f_hi = min(P / 4, F - 1);
   for (int f = max(0, (P - 12) / 4); f <= f_hi; ++f) {
@@ -402,10 +412,17 @@ __global__ __launch_bounds__(256) void istft_ola_kernel(const float* __restrict_
   out[n] = fminf(fmaxf(v, -limit), limit);
 }
 
+__global__ __launch_bounds__(256) void copy_live_kernel(const float* __restrict__ src,
+                                                        float* __restrict__ dst,
+                                                        const HiftDocs* __restrict__ docs) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < docs->b[docs->n]) dst[i] = src[i];
+}
+
 unsigned blocks_for(long n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
 template <typename T>
-hipError_t launch_conv(const HiftConv& p, const HiftDocs& docs, hipStream_t stream) {
+hipError_t launch_conv(const HiftConv& p, const HiftDocs* docs, hipStream_t stream) {
   if (p.rows_out <= 0) return hipSuccess;
   if (p.cin_pad % 16 != 0) return hipErrorInvalidValue;
   const dim3 grid((p.rows_out + kTileR - 1) / kTileR, (p.cout + kTileC - 1) / kTileC);
@@ -418,66 +435,79 @@ hipError_t launch_conv(const HiftConv& p, const HiftDocs& docs, hipStream_t stre
 
 }  // namespace
 
-hipError_t hift_conv_f32(const HiftConv& p, const HiftDocs& docs, hipStream_t stream) {
+hipError_t hift_conv_f32(const HiftConv& p, const HiftDocs* docs, hipStream_t stream) {
   return launch_conv<float>(p, docs, stream);
 }
-hipError_t hift_conv_f64(const HiftConv& p, const HiftDocs& docs, hipStream_t stream) {
+hipError_t hift_conv_f64(const HiftConv& p, const HiftDocs* docs, hipStream_t stream) {
   return launch_conv<double>(p, docs, stream);
 }
 
 hipError_t hift_snake(const float* x, int ldx, float* out, int ldo, int rows, int C,
-                      const float* alpha, const float* inv_alpha, hipStream_t stream) {
+                      const float* alpha, const float* inv_alpha, const HiftDocs* docs,
+                      hipStream_t stream) {
   if (rows <= 0) return hipSuccess;
   const long n = (long)rows * (C / 4);
   hipLaunchKernelGGL(snake_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, x, ldx, out,
-                     ldo, rows, C, alpha, inv_alpha);
+                     ldo, C, alpha, inv_alpha, docs);
   return hipGetLastError();
 }
 
-hipError_t hift_to_f64(const float* x, double* y, long n, hipStream_t stream) {
+hipError_t hift_to_f64(const float* x, double* y, int rows, int C, const HiftDocs* docs,
+                       hipStream_t stream) {
+  const long n = (long)rows * C;
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(to_f64_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, x, y, n);
+  hipLaunchKernelGGL(to_f64_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, x, y, C,
+                     docs);
   return hipGetLastError();
 }
 
 hipError_t hift_f0_head(const double* h, int C, const double* cls_w, const double* cls_b,
-                        int rows, float* f0, hipStream_t stream) {
+                        int rows, float* f0, const HiftDocs* docs, hipStream_t stream) {
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(f0_head_kernel, dim3(rows), dim3(64), 0, stream, h, C, cls_w, cls_b, f0);
+  hipLaunchKernelGGL(f0_head_kernel, dim3(rows), dim3(64), 0, stream, h, C, cls_w, cls_b, f0,
+                     docs);
   return hipGetLastError();
 }
 
-hipError_t hift_source(const HiftSource& p, const HiftDocs& docs, hipStream_t stream) {
-  hipLaunchKernelGGL(source_phase_kernel, dim3(p.n_docs), dim3(64), 0, stream, p, docs);
+hipError_t hift_source(const HiftSource& p, const HiftDocs* docs, hipStream_t stream) {
+  if (p.docs_cap <= 0) return hipSuccess;
+  hipLaunchKernelGGL(source_phase_kernel, dim3(p.docs_cap), dim3(64), 0, stream, p, docs);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int samples = docs.b[p.n_docs];
-  if (samples <= 0) return hipSuccess;
-  hipLaunchKernelGGL(source_sample_kernel, dim3(blocks_for(samples, 256)), dim3(256), 0, stream,
-                     p, docs, samples);
+  if (p.samples_cap <= 0) return hipSuccess;
+  hipLaunchKernelGGL(source_sample_kernel, dim3(blocks_for(p.samples_cap, 256)), dim3(256), 0,
+                     stream, p, docs);
   return hipGetLastError();
 }
 
-hipError_t hift_stft(const float* s, const float* window, float* out, int ld, int n_docs,
-                     int frames, const HiftDocs& docs, hipStream_t stream) {
+hipError_t hift_copy_live(const float* src, float* dst, int rows, const HiftDocs* docs,
+                          hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(copy_live_kernel, dim3(blocks_for(rows, 256)), dim3(256), 0, stream, src,
+                     dst, docs);
+  return hipGetLastError();
+}
+
+hipError_t hift_stft(const float* s, const float* window, float* out, int ld, int frames,
+                     const HiftDocs* docs, hipStream_t stream) {
   if (frames <= 0) return hipSuccess;
   hipLaunchKernelGGL(stft_kernel, dim3(blocks_for(frames, 256)), dim3(256), 0, stream, s, window,
-                     out, ld, n_docs, frames, docs);
+                     out, ld, docs);
   return hipGetLastError();
 }
 
 hipError_t hift_istft(const float* y, int ldy, const float* window, float* fr, float* out,
-                      float limit, int n_docs, int frames, int samples, const HiftDocs& docs,
+                      float limit, int frames, int samples, const HiftDocs* docs,
                       hipStream_t stream) {
   if (frames > 0) {
     hipLaunchKernelGGL(istft_frame_kernel, dim3(blocks_for(frames, 256)), dim3(256), 0, stream, y,
-                       ldy, window, fr, frames);
+                       ldy, window, fr, docs);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (samples <= 0) return hipSuccess;
   hipLaunchKernelGGL(istft_ola_kernel, dim3(blocks_for(samples, 256)), dim3(256), 0, stream, fr,
-                     window, out, limit, n_docs, samples, docs);
+                     window, out, limit, docs);
   return hipGetLastError();
 }
 

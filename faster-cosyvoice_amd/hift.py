@@ -29,6 +29,27 @@ def _ceil(v: int, m: int) -> int:
     return (v + m - 1) // m * m
 
 
+def capacity_bucket(frames: int, n_docs: int) -> tuple[int, int]:
+    """The capacity a packed vocoder call of ``frames`` Mel frames in ``n_docs`` requests is
+    run in: frames rounded up to m * 2^e with m in 8..15 (at most 12.5 % above, at least 64),
+    requests to a power of two.  Calls in one bucket share its captured graph."""
+    cap = 64
+    while cap < frames:
+        cap *= 2
+    low = cap // 2
+    for m in range(9, 17):
+        if m * low // 8 >= frames:
+            cap = max(64, m * low // 8)
+            break
+    docs = 1
+    while docs < n_docs:
+        docs *= 2
+    return cap, docs
+
+
+_BUFFER_SETS = 4  # per lane: one buffer set per vocoder graph its handle can pool
+
+
 class HiFTVocoder:
     """Packed-batch HiFT vocoder on gfx950 HIP kernels (CausalHiFTGenerator counterpart)."""
 
@@ -192,7 +213,8 @@ class HiFTVocoder:
                 h = _lib.c_void_p()
                 _lib.check(self._lib.fcv_hift_create(self._cdims, self._ptrs, len(self._ptrs), h))
                 handle = h.value
-            self._lanes.append([handle, None, group_stream(self.device, len(self._lanes))])
+            # [handle, workspace, stream, buffer sets by capacity]
+            self._lanes.append([handle, None, group_stream(self.device, len(self._lanes)), {}])
         return self._lanes[i]
 
     def _require(self) -> int:
@@ -209,9 +231,36 @@ class HiFTVocoder:
                              f"{'final' if finalize else 'non-final'} chunk")
         return n
 
+    def graph_stats(self, group: int = 0) -> tuple[int, int]:
+        """(vocoder graphs held, calls captured so far) of request group ``group``'s handle."""
+        pooled, captures = _lib.c_int32(), _lib.c_int32()
+        _lib.check(self._lib.fcv_hift_graph_stats(self._lane(group)[0], pooled, captures))
+        return pooled.value, captures.value
+
+    def _buffers(self, lane: list, cap: tuple[int, int], return_source: bool) -> dict:
+        """The lane's input and output buffers for capacity ``cap`` (kept per capacity, so the
+        pointers a captured graph was recorded with come back with its capacity)."""
+        sets = lane[3]
+        key = (cap, return_source)
+        bufs = sets.pop(key, None)
+        if bufs is None:
+            frames, docs = cap
+            scale = self.dims.upsample_scale
+            f32 = lambda n: torch.empty(max(n, 1), dtype=torch.float32, device=self.device)
+            bufs = {"mel": torch.zeros(frames, self.dims.in_channels, dtype=torch.float32,
+                                       device=self.device),
+                    "speech": f32(scale * frames + self.dims.hop_len * docs),
+                    "source": f32(scale * frames) if return_source else None}
+            while len(sets) >= _BUFFER_SETS:
+                sets.pop(next(iter(sets)))
+        sets[key] = bufs
+        return bufs
+
     def _run(self, lane: list, mels: list[torch.Tensor], fin: list[bool], return_source: bool,
-             stream: int) -> tuple[list, list]:
-        """Packed calls of at most HIFT_MAX_DOCS requests on ``lane``, enqueued on ``stream``."""
+             stream: int, graph: bool = True) -> tuple[list, list]:
+        """Packed calls of at most HIFT_MAX_DOCS requests on ``lane``, enqueued on ``stream``.
+        Each call runs in its capacity bucket (``capacity_bucket``) from the lane's buffers for
+        that capacity; with ``graph`` the capacity's captured graph replays it."""
         h = lane[0]
         speech_all, source_all = [], []
         for g0 in range(0, len(mels), _lib.HIFT_MAX_DOCS):
@@ -221,27 +270,34 @@ class HiFTVocoder:
             samples = [self.output_samples(t, f) for t, f in zip(frames, gfin)]
             f0_frames = [t if f else t - 3 for t, f in zip(frames, gfin)]
             src_len = [t * self.dims.upsample_scale for t in f0_frames]
-            x = torch.cat([m.to(self.device, torch.float32).transpose(0, 1) for m in group])
-            x = x.contiguous()
+            cap = capacity_bucket(sum(frames), len(group))
+            bufs = self._buffers(lane, cap, return_source)
+            off = 0
+            for m in group:
+                n = int(m.shape[1])
+                bufs["mel"][off:off + n].copy_(m.to(self.device, torch.float32).transpose(0, 1))
+                off += n
             fr = (_lib.c_int32 * len(group))(*frames)
             fl = (_lib.c_int32 * len(group))(*[int(f) for f in gfin])
-            need = int(self._lib.fcv_hift_workspace_bytes(h, fr, fl, len(group)))
+            need = int(self._lib.fcv_hift_workspace_bytes_capacity(h, cap[0], cap[1]))
             if need == 0:
                 raise ValueError("bad HiFT call layout")
             if lane[1] is None or lane[1].numel() < need:
+                lane[1] = None
                 lane[1] = torch.empty(need, dtype=torch.uint8, device=self.device)
-            speech = torch.empty(max(sum(samples), 1), dtype=torch.float32, device=self.device)
-            source = (torch.empty(max(sum(src_len), 1), dtype=torch.float32, device=self.device)
-                      if return_source else None)
-            _lib.check(self._lib.fcv_hift_inference(
-                h, x.data_ptr(), fr, fl, len(group), speech.data_ptr(),
-                source.data_ptr() if source is not None else None, lane[1].data_ptr(),
-                lane[1].numel(), stream))
+            source = bufs["source"]
+            _lib.check(self._lib.fcv_hift_inference_capacity(
+                h, bufs["mel"].data_ptr(), fr, fl, len(group), cap[0], cap[1],
+                bufs["speech"].data_ptr(), source.data_ptr() if source is not None else None,
+                lane[1].data_ptr(), lane[1].numel(), int(bool(graph)), stream))
+            # the buffers are the lane's: the next call writes them again
+            speech = bufs["speech"][:sum(samples)].clone()
             off = 0
             for n in samples:
                 speech_all.append(speech[off:off + n].view(1, n))
                 off += n
             if source is not None:
+                source = source[:sum(src_len)].clone()
                 off = 0
                 for n in src_len:
                     source_all.append(source[off:off + n].view(1, 1, n))
@@ -251,7 +307,8 @@ class HiFTVocoder:
     @torch.no_grad()
     def inference_batched(self, mels: Sequence[torch.Tensor],
                           finalize_list: Sequence[bool] | None = None,
-                          return_source: bool = False, concurrency: int | None = None):
+                          return_source: bool = False, concurrency: int | None = None,
+                          graph: bool = True):
         """Vocode requests of different lengths in packed passes.  ``mels``: each ``[80, T]``
         or ``[1, 80, T]``.  Returns one ``[1, N]`` fp32 waveform per request (and the
         ``[1, 1, L]`` sources with ``return_source``).  Each waveform equals what
@@ -260,7 +317,11 @@ class HiFTVocoder:
         The requests run as ``concurrency`` groups (default: 2 when there are at least 2),
         balanced by Mel frames, each a packed call on its own handle over the shared weights
         and its own stream, all in flight together (one packed call of 8 requests at config 3:
-        23.5 ms; two groups: 22.1 ms)."""
+        23.5 ms; two groups: 22.1 ms).
+
+        Each call runs in a capacity bucket (``capacity_bucket``); with ``graph`` the launch
+        sequence is captured on a bucket's second call and replayed for every later layout in
+        it (fcv_hift_inference_capacity), bit-identical to an eager call."""
         self._require()
         mels = [m.reshape(m.shape[-2], m.shape[-1]) for m in mels]
         if not mels:
@@ -287,7 +348,7 @@ class HiFTVocoder:
         for lane, g in zip(lanes, groups):
             with torch.cuda.stream(lane[2]):
                 results.append(self._run(lane, [mels[i] for i in g], [fin[i] for i in g],
-                                         return_source, lane[2].cuda_stream))
+                                         return_source, lane[2].cuda_stream, graph))
         for lane in lanes:
             current.wait_stream(lane[2])
         speech_all: list = [None] * len(mels)

@@ -98,6 +98,29 @@ int fcv_hift_inference(FcvHift* hift, const float* mel, const int32_t* frames_ho
                        float* source_out, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
 
+/* Device workspace of a call capacity: at most frames_cap Mel frames in docs_cap documents. */
+size_t fcv_hift_workspace_bytes_capacity(const FcvHift* hift, int32_t frames_cap,
+                                         int32_t docs_cap);
+
+/* fcv_hift_inference inside a capacity (sum of frames <= frames_cap, n_docs <= docs_cap), with
+ * the graph pool: replaces the reference's per-bucket CUDA graphs of the streaming vocoder
+ * (hift_graph.py:65-169; HiftStreamGraph pads each request to its bucket and replays).  The
+ * workspace carve-up and every grid depend on the capacity only; the call's layout is written
+ * into the workspace and read by the kernels, so with use_graph != 0 the launch sequence
+ * captured for (capacity, workspace, mel, speech_out, source_out) replays for any later layout
+ * of that capacity, bit-identical to an eager call.  A key is captured on its second call; the
+ * handle keeps the 4 most recently used graphs.  The layout is copied from host memory on
+ * `stream` before the launches (the copy is complete when the call returns). */
+int fcv_hift_inference_capacity(FcvHift* hift, const float* mel, const int32_t* frames_host,
+                                const int32_t* finalize_host, int32_t n_docs, int32_t frames_cap,
+                                int32_t docs_cap, float* speech_out, float* source_out,
+                                void* workspace, size_t workspace_bytes, int32_t use_graph,
+                                hipStream_t stream);
+
+/* Vocoder graphs the handle holds (at most 4) and the calls it has captured so far.  No
+ * counterpart in the reference (whose graph runner logs each capture, hift_graph.py:136-137). */
+int fcv_hift_graph_stats(const FcvHift* hift, int32_t* pooled, int32_t* captures);
+
 #ifdef __cplusplus
 }
 #endif

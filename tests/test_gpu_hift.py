@@ -98,3 +98,27 @@ def test_short_non_final_chunk_is_rejected(hift):
     _, _, _, v = hift
     with pytest.raises(ValueError):
         v.inference_batched([torch.zeros(80, 7, device="cuda")], [False])
+
+
+def test_vocoder_graph_replays_new_layouts(fcv, hift):
+    """Calls in one capacity bucket share one captured graph: a layout never seen before
+    replays it with no new capture and gives bit for bit the eager call's waveforms and
+    sources; a call in another bucket captures its own graph (the reference's per-bucket
+    streaming vocoder graphs, hift_graph.py:65-169)."""
+    _, _, _, v = hift
+    g = torch.Generator().manual_seed(78)
+    calls = {"A": ([40, 20], [False, True]), "B": ([30, 33], [True, False]),
+             "C": ([9, 12, 20], [False, True, True])}
+    mels = {k: [torch.randn(80, n, generator=g).cuda() for n in f] for k, (f, _) in calls.items()}
+    cap = {k: fcv.hift.capacity_bucket(sum(f), len(f)) for k, (f, _) in calls.items()}
+    assert cap["A"] == cap["B"] == (64, 2) and cap["C"] == (64, 4)
+    run = lambda k, graph: v.inference_batched(mels[k], calls[k][1], return_source=True,
+                                               concurrency=1, graph=graph)
+    eager = {k: run(k, False) for k in calls}
+    _, c0 = v.graph_stats()
+    for name, captures in [("A", 0), ("A", 1), ("B", 1), ("C", 1), ("C", 2), ("B", 2), ("A", 2)]:
+        say(f"[hift graph] call {name}")
+        speech, source = run(name, True)
+        assert all(torch.equal(a, b) for a, b in zip(speech, eager[name][0])), name
+        assert all(torch.equal(a, b) for a, b in zip(source, eager[name][1])), name
+        assert v.graph_stats()[1] - c0 == captures, name
