@@ -43,7 +43,7 @@ struct Layout {
   // byte offsets inside the workspace
   size_t h, nbuf, obuf, q, k, vt, u, ain, vbuf;
   size_t docid, pos, ext_row, docid_ext, pos_ext, cu_int, lens, cu_ext, tiles, live;
-  size_t mod, tsin, t1, t2, tbuf;
+  size_t mod, tsin, t1, t2, tbuf, fold, hstat;
   size_t total;
 };
 
@@ -53,6 +53,9 @@ long internal_rows_bound(long rows, long n_docs) { return rows + 7 * n_docs; }
 long tiles_bound(long rows, long n_docs) {
   return internal_rows_bound(rows, n_docs) / fcv::kAttnTileQ + n_docs + 1;
 }
+
+// floats of adaln_fold's output per modulation row
+long fold_width(const FcvDitDims& d) { return (long)d.depth * (6L * d.dim + 2L * d.ff_dim); }
 
 // Workspace of a capacity: at most `rows` caller rows in at most `n_docs` documents.
 Layout make_layout(const FcvDitDims& d, long rows, long n_docs) {
@@ -93,6 +96,9 @@ Layout make_layout(const FcvDitDims& d, long rows, long n_docs) {
   L.t1 = take(nt * (long)d.dim * 2);
   L.t2 = take(nt * (long)d.dim * 2);
   L.tbuf = take(kMaxSteps * 4);
+  // LayerNorm fold: column terms per step of a group (adaln_fold), row statistics per row
+  L.fold = take((long)kModGroup * fold_width(d) * 4);
+  L.hstat = take(rp * (long)fcv::kStatChunks * 8);
   L.total = off;
   return L;
 }
@@ -172,8 +178,9 @@ namespace {
 
 // timestep embedding -> SiLU(temb) -> every block's AdaLN modulation in one projection, for
 // n_t time values: row i of the `mod` region (mod_width floats) belongs to t[i]
-// (TimestepEmbedding modules.py:606-616; _project_modulations flashinfer_dit.py:430-445)
-int compute_modulations(FcvDit* m, const float* t, int n_t, hipStream_t s) {
+// (TimestepEmbedding modules.py:606-616; _project_modulations flashinfer_dit.py:430-445).
+// With `fold` (n_t <= kModGroup), also the LayerNorm fold's column terms of each row.
+int compute_modulations(FcvDit* m, const float* t, int n_t, bool fold, hipStream_t s) {
   const FcvDitWeights& w = m->w;
   const int D = m->dims.dim;
   auto B = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
@@ -188,34 +195,49 @@ int compute_modulations(FcvDit* m, const float* t, int n_t, hipStream_t s) {
   for (int rep = m->launches(FCV_STAGE_ADALN, -1); rep > 0; --rep)
     FCV_HIP(fcv::gemm_bias_f32(t2, D, B(w.ada_w), D, w.ada_b, n_t, (int)m->mod_width, D, mod,
                                (int)m->mod_width, (int)m->mod_width, s));
+  if (fold)
+    FCV_HIP(fcv::adaln_fold(B(w.qkv_w), w.qkv_b, B(w.ff1_w), w.ff1_b, m->dims.depth, D,
+                            m->dims.ff_dim, mod, m->mod_width, n_t, m->at<float>(m->L.fold), s));
   FCV_HIP(m->probe_end(FCV_STAGE_ADALN, -1, s));
   return FCV_OK;
 }
 
 int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
-               const float* mod, long mod_stride, float* v_out, hipStream_t s);
+               const float* mod, long mod_stride, const float* fold, float* v_out, hipStream_t s);
 
 // one estimator evaluation: modulations for t (1 shared value or one per document), then the
-// network; `mod_row`, when not null, is an already computed shared-t modulation row
+// network; `mod_row`, when not null, is an already computed shared-t modulation row and
+// `fold_row` its LayerNorm fold terms
 int run_forward(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
-                const float* t, int n_t, const float* mod_row, float* v_out, hipStream_t s) {
+                const float* t, int n_t, const float* mod_row, const float* fold_row,
+                float* v_out, hipStream_t s) {
   FCV_HIP(m->probe_begin(FCV_STAGE_FORWARD, -1, s));
   const float* mod = mod_row;
+  const float* fold = fold_row;
   long mod_stride = 0;
   if (!mod) {
-    int rc = compute_modulations(m, t, n_t, s);
+    // one t for every document: the LayerNorms fold into the GEMMs; one t per document: they
+    // run as LN-modulate passes
+    int rc = compute_modulations(m, t, n_t, n_t == 1, s);
     if (rc != FCV_OK) return rc;
     mod = m->at<float>(m->L.mod);
     mod_stride = (n_t == 1) ? 0 : m->mod_width;
+    fold = (n_t == 1) ? m->at<float>(m->L.fold) : nullptr;
   }
-  int rc = run_blocks(m, x, mu, cond, spks, mod, mod_stride, v_out, s);
+  int rc = run_blocks(m, x, mu, cond, spks, mod, mod_stride, fold, v_out, s);
   if (rc != FCV_OK) return rc;
   FCV_HIP(m->probe_end(FCV_STAGE_FORWARD, -1, s));
   return FCV_OK;
 }
 
+// `fold` (mod_stride 0 only): adaln_fold's terms for the modulation row.  Then the LayerNorm
+// before every GEMM but the first block's QKV and proj_out runs inside the GEMMs: each gated
+// residual writes bf16(h * g) of the next LayerNorm and h's row statistics, and the next QKV or
+// FF1 GEMM applies the normalization in its epilogue.  Without it, each LayerNorm + modulation
+// is a pass of its own (ln_mod_kernel) that writes the GEMM's normalized bf16 input.
 int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
-               const float* mod, long mod_stride, float* v_out, hipStream_t s) {
+               const float* mod, long mod_stride, const float* fold, float* v_out,
+               hipStream_t s) {
   const FcvDitDims& d = m->dims;
   const FcvDitWeights& w = m->w;
   // grids cover the plan's capacity; the kernels read the live counts
@@ -238,6 +260,9 @@ int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, co
   int32_t* cu_int = m->at<int32_t>(m->L.cu_int);
   int32_t* lens = m->at<int32_t>(m->L.lens);
   int32_t* tiles = m->at<int32_t>(m->L.tiles);
+  float2* hstat = m->at<float2>(m->L.hstat);
+  const bool folded = fold != nullptr && mod_stride == 0;
+  const long fw = 6L * D + 2L * F;  // fold terms per block: u_qkv, v_qkv, u_ff1, v_ff1
 
   // input projection + causal conv position embedding (InputEmbedding dit.py:84-98)
   FCV_HIP(fcv::pack_inputs(x, cond, mu, spks, docid, ext_row, R, mel, ain, s, live_rows));
@@ -257,17 +282,22 @@ int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, co
   // transformer blocks (DiTBlock.forward modules.py:516-530)
   for (int l = 0; l < d.depth; ++l) {
     const long base = (long)l * 6 * D;
-    FCV_HIP(m->probe_begin(FCV_STAGE_LN_MOD, l, s));
-    for (int rep = m->launches(FCV_STAGE_LN_MOD, l); rep > 0; --rep)
-      FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 0), (int)(base + D),
-                                       docid, nbuf, s, live_rows));
-    FCV_HIP(m->probe_end(FCV_STAGE_LN_MOD, l, s));
+    const float* fl = folded ? fold + l * fw : nullptr;
+    const bool fold_qkv = folded && l > 0;  // block 0's input comes from the conv, not a GEMM
+    if (!fold_qkv) {
+      FCV_HIP(m->probe_begin(FCV_STAGE_LN_MOD, l, s));
+      for (int rep = m->launches(FCV_STAGE_LN_MOD, l); rep > 0; --rep)
+        FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 0),
+                                         (int)(base + D), docid, nbuf, s, live_rows));
+      FCV_HIP(m->probe_end(FCV_STAGE_LN_MOD, l, s));
+    }
     FCV_HIP(m->probe_begin(FCV_STAGE_QKV, l, s));
     for (int rep = m->launches(FCV_STAGE_QKV, l); rep > 0; --rep)
       FCV_HIP(fcv::gemm_qkv_rope(nbuf, D, B(w.qkv_w) + (long)l * 3 * D * D, D,
-                                 w.qkv_b + (long)l * 3 * D, R, D, d.heads, pos, w.rope_cos,
-                                 w.rope_sin, d.rope_dim, d.max_pos, q, k, vt, m->rp, s,
-                                 live_rows));
+                                 fold_qkv ? fl + 3 * D : w.qkv_b + (long)l * 3 * D, R, D, d.heads,
+                                 pos, w.rope_cos, w.rope_sin, d.rope_dim, d.max_pos, q, k, vt,
+                                 m->rp, s, live_rows, fold_qkv ? fl : nullptr,
+                                 fold_qkv ? hstat : nullptr));
     FCV_HIP(m->probe_end(FCV_STAGE_QKV, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_ATTENTION, l, s));
     for (int rep = m->launches(FCV_STAGE_ATTENTION, l); rep > 0; --rep)
@@ -278,19 +308,26 @@ int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, co
     FCV_HIP(m->probe_begin(FCV_STAGE_OUT_PROJ, l, s));
     FCV_HIP(fcv::gemm_gated_residual(obuf, D, B(w.out_w) + (long)l * D * D, D,
                                      w.out_b + (long)l * D, R, D, D, h, D, mod + base + 2 * D,
-                                     mod_stride, docid, s, live_rows));
+                                     mod_stride, docid, s, live_rows,
+                                     folded ? mod + base + 4 * D : nullptr, nbuf, hstat));
     FCV_HIP(m->probe_end(FCV_STAGE_OUT_PROJ, l, s));
-    FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 3 * D),
-                                     (int)(base + 4 * D), docid, nbuf, s, live_rows));
+    if (!folded)
+      FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 3 * D),
+                                       (int)(base + 4 * D), docid, nbuf, s, live_rows));
     FCV_HIP(m->probe_begin(FCV_STAGE_FF1, l, s));
     for (int rep = m->launches(FCV_STAGE_FF1, l); rep > 0; --rep)
       FCV_HIP(fcv::gemm_bias_gelu_bf16(nbuf, D, B(w.ff1_w) + (long)l * F * D, D,
-                                       w.ff1_b + (long)l * F, R, F, D, u, F, s, live_rows));
+                                       folded ? fl + 6 * D + F : w.ff1_b + (long)l * F, R, F, D,
+                                       u, F, s, live_rows, folded ? fl + 6 * D : nullptr,
+                                       folded ? hstat : nullptr));
     FCV_HIP(m->probe_end(FCV_STAGE_FF1, l, s));
+    // the next block's attention LayerNorm folds into this gated residual (not after the last)
+    const bool fold_next = folded && l + 1 < d.depth;
     FCV_HIP(m->probe_begin(FCV_STAGE_FF2, l, s));
     FCV_HIP(fcv::gemm_gated_residual(u, F, B(w.ff2_w) + (long)l * D * F, F,
                                      w.ff2_b + (long)l * D, R, D, F, h, D, mod + base + 5 * D,
-                                     mod_stride, docid, s, live_rows));
+                                     mod_stride, docid, s, live_rows,
+                                     fold_next ? mod + base + 6 * D + D : nullptr, nbuf, hstat));
     FCV_HIP(m->probe_end(FCV_STAGE_FF2, l, s));
   }
 
@@ -495,7 +532,7 @@ int fcv_dit_forward(FcvDit* m, const float* x, const float* mu, const float* con
             "spks and cond are required (null input pointer)");
   FCV_CHECK(n_t == 1 || n_t == m->n_docs, FCV_ERR_INVALID, "n_t must be 1 or n_docs");
   m->probe_count = 0;
-  return run_forward(m, x, mu, cond, spks, t, n_t, nullptr, v_out, s);
+  return run_forward(m, x, mu, cond, spks, t, n_t, nullptr, nullptr, v_out, s);
 }
 
 static int check_cfg_layout(const FcvDit* m) {
@@ -535,14 +572,17 @@ int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const
   auto body = [&]() -> int {
     m->probe_count = 0;
     const float* mod = m->at<float>(m->L.mod);
+    const float* fold = m->at<float>(m->L.fold);
     for (int step = 0; step < n_steps; ++step) {
       // every kModGroup steps, one pass over the AdaLN weights gives the next steps' rows
       if (step % kModGroup == 0) {
-        int r = compute_modulations(m, tbuf + step, std::min(kModGroup, n_steps - step), s);
+        int r = compute_modulations(m, tbuf + step, std::min(kModGroup, n_steps - step), true,
+                                    s);
         if (r != FCV_OK) return r;
       }
-      int r = run_forward(m, x, mu, cond, spks, nullptr, 1, mod + (step % kModGroup) * m->mod_width,
-                          vbuf, s);
+      const int row = step % kModGroup;
+      int r = run_forward(m, x, mu, cond, spks, nullptr, 1, mod + row * m->mod_width,
+                          fold + row * fold_width(m->dims), vbuf, s);
       if (r != FCV_OK) return r;
       FCV_HIP(m->probe_begin(FCV_STAGE_EULER, -1, s));
       FCV_HIP(fcv::euler_cfg_update(x, vbuf, m->rc_cap, mel, dt_host[step], cfg, s,

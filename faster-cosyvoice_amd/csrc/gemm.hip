@@ -22,6 +22,13 @@
 // at a time (16-byte fp32 / 8-byte bf16 vector accesses), and the interleaved RoPE pairs
 // (2i, 2i+1) sit in the same lane.
 //
+// LayerNorm fold (kFold): the A operand is bf16(x * g) for a residual row x and the next
+// LayerNorm's scale row g, written by the gated-residual epilogue that produced x together with
+// per-row statistics of x in 32-column chunks.  The prologue combines each of the tile's rows'
+// chunks into (rs, -mu * rs) in LDS; the epilogue turns the accumulator into
+// rs * acc - mu * rs * u[col] (u = W . g), and the epilogue's bias is W . shift + bias.  That is
+// LN(x) * g + shift projected by W, without the normalized rows ever reaching memory.
+//
 // Rasterization: blocks are dealt round-robin over the 8 XCDs, so block ids are first remapped
 // to give each XCD a contiguous range of tiles; inside that range tiles are visited in groups of
 // GROUP_M M-tiles x all N-tiles (M fastest), keeping the group's A rows and W columns inside
@@ -122,13 +129,65 @@ __device__ __forceinline__ void wait_loads_ahead(int ahead) {
   }
 }
 
-template <class C, class Epi>
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+// The fold's inputs: per-row chunk statistics (kStatChunks x (sum, centered sum of squares))
+// and u = W . g per output column.
+struct FoldArgs {
+  const float2* stats;
+  const float* u;
+};
+
+// v from the lane a DPP control names (bound_ctrl off: every source lane exists here)
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+// sums over aligned groups of 8 and 16 lanes: two quad swaps, the half-row mirror (lane i adds
+// lane 7 - i, which holds the other quad's sum) and the row mirror (lane i adds lane 15 - i);
+// every lane of a group ends with the same value
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  return v;
+}
+__device__ __forceinline__ float sum16(float v) {
+  const float h = sum8(v);
+  return h + dpp<0x140>(h);  // row_mirror
+}
+
+// (rs, -mu * rs) of one row from its chunk statistics, spread over an aligned group of 16 lanes
+// (lane j holds chunks 2j and 2j+1 as (sum, M2, sum, M2)): Chan et al.'s pairwise update
+// M2 = sum_c (M2_c + n_c (mean_c - mean)^2), eps 1e-6, biased variance.  Every lane of the
+// group gets the result.
+__device__ __forceinline__ float2 row_affine(const float4& c) {
+  constexpr float kN = 32.0f * kStatChunks;
+  const float mu = sum16(c.x + c.z) * (1.0f / kN);
+  const float d0 = c.x - 32.0f * mu, d1 = c.z - 32.0f * mu;
+  const float m2 = sum16((c.y + d0 * d0 * (1.0f / 32.0f)) + (c.w + d1 * d1 * (1.0f / 32.0f)));
+  const float rs = rsqrtf(m2 * (1.0f / kN) + 1e-6f);
+  return float2{rs, -mu * rs};
+}
+
+// rs * acc + (-mu * rs * u + bias): the folded LayerNorm and the epilogue's bias
+__device__ __forceinline__ float4 fold4(const f32x4& v, float2 a, const float4& u, const float4& b) {
+  return float4{fmaf(a.x, v[0], fmaf(a.y, u.x, b.x)), fmaf(a.x, v[1], fmaf(a.y, u.y, b.y)),
+                fmaf(a.x, v[2], fmaf(a.y, u.z, b.z)), fmaf(a.x, v[3], fmaf(a.y, u.w, b.w))};
+}
+
+template <class C, class Epi, bool kFold>
 __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
     const bf16* __restrict__ A, int lda, const bf16* __restrict__ W, int ldw, int M, int N, int K,
-    Epi epi, const int32_t* __restrict__ m_live) {
+    Epi epi, const int32_t* __restrict__ m_live, FoldArgs fold) {
   constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN, BK = C::BK, S = C::STAGES;
+  // fold: 16 lanes per row's statistics, kStatRows rows per pass of the workgroup
+  constexpr int kStatRows = C::kThreads / 16;
+  constexpr int kStatPasses = kFold ? (BM + kStatRows - 1) / kStatRows : 1;
+  static_assert(kStatChunks == 32, "16 lanes x 2 chunks per row");
   // operand ring; after the K loop the same bytes stage the epilogue
   __shared__ __attribute__((aligned(1024))) bf16 smem[S * (BM + BN) * BK];
+  __shared__ float2 rstat[kFold ? BM : 1];  // (rs, -mu * rs) of the tile's rows
   bf16 (*sA)[BM * BK] = reinterpret_cast<bf16 (*)[BM * BK]>(smem);
   bf16 (*sB)[BN * BK] = reinterpret_cast<bf16 (*)[BN * BK]>(smem + S * BM * BK);
 
@@ -140,6 +199,18 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   const int m0 = tmi * BM;
   const int n0 = tni * BN;
   const int lane = threadIdx.x & 63;
+  // fold: the tile's rows' chunk statistics (rows past M take row M - 1's, as the A copies do),
+  // fetched ahead of the operand copies so the wait for the first slice covers them; a pass
+  // reads kStatRows consecutive rows as one contiguous span
+  float4 stat_in[kStatPasses];
+  if constexpr (kFold) {
+#pragma unroll
+    for (int p = 0; p < kStatPasses; ++p) {
+      const int r = min(p * kStatRows + (int)threadIdx.x / 16, BM - 1);
+      stat_in[p] = reinterpret_cast<const float4*>(
+          fold.stats + (long)min(m0 + r, M - 1) * kStatChunks)[threadIdx.x & 15];
+    }
+  }
   // wave index as a scalar, so the copies' LDS destinations are computed in SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm0 = (wave / C::WN) * (BM / C::WM);
@@ -190,6 +261,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   const int rc = (lane % LANES_PER_ROW) * 4;
   Col scol{};
   Col dcol[TN][4];
+  float4 sfold{};
   if (direct) {
 #pragma unroll
     for (int j = 0; j < TN; ++j)
@@ -197,6 +269,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
       for (int g = 0; g < 4; ++g) dcol[j][g] = epi.column(col_base + j * 32 + g * 8 + (lane >> 5) * 4);
   } else {
     scol = epi.column(col_base + rc);
+    if constexpr (kFold) sfold = ld4(fold.u + col_base + rc);
   }
 
   f32x16 acc[TM][TN];
@@ -260,6 +333,14 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   for (int st = 0; st < S - 1; ++st)
     if (st < KT) issue(st, st);
   wait_loads_ahead<C::LOADS, S - 2>(KT - 1);  // slice 0
+  if constexpr (kFold) {
+#pragma unroll
+    for (int p = 0; p < kStatPasses; ++p) {
+      const float2 a = row_affine(stat_in[p]);
+      const int r = p * kStatRows + (int)threadIdx.x / 16;
+      if ((threadIdx.x & 15) == 0 && r < BM) rstat[r] = a;
+    }
+  }
   __syncthreads();
   if (S - 1 < KT) issue(S - 1, S - 1);
   load(0, 0, 0);
@@ -296,19 +377,33 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   constexpr int PITCH = WCOLS + 4;  // floats
   static_assert(C::kWaves * 32 * PITCH * 4 <= (int)sizeof(smem), "epilogue staging");
   if (direct) {
-    // direct-layout tiles (V^T) read nothing per row
+    // direct-layout tiles (V^T) read nothing per row; the fold's u columns are read here, one
+    // 32-column block at a time, not before the K loop, where they would stay live in registers
+    // through it (nothing has been stored yet, so these loads wait for nothing else)
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int row = m0 + wm0 + i * 32 + fr;
+    for (int j = 0; j < TN; ++j) {
+      float4 ufold[kFold ? 4 : 1];
+      if constexpr (kFold) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+        for (int g = 0; g < 4; ++g) ufold[g] = ld4(fold.u + col_base + j * 32 + g * 8 + fh * 4);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = m0 + wm0 + i * 32 + fr;
+        float2 aff{1.0f, 0.0f};
+        if constexpr (kFold) aff = rstat[wm0 + i * 32 + fr];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                            acc[i][j][4 * g + 3]};
-          epi.finish(v, epi.blank(dcol[j][g]), dcol[j][g], row,
-                     col_base + j * 32 + g * 8 + fh * 4, M);
+          const int c = col_base + j * 32 + g * 8 + fh * 4;
+          if constexpr (kFold)
+            epi.finish_biased(fold4(v, aff, ufold[g], dcol[j][g].b), epi.blank(dcol[j][g]),
+                              dcol[j][g], row, c, M);
+          else
+            epi.finish(v, epi.blank(dcol[j][g]), dcol[j][g], row, c, M);
         }
+      }
     }
     return;
   }
@@ -348,8 +443,14 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-      for (int p = 0; p < PASSES; ++p)
-        epi.finish(v[p], cx[p], scol, m0 + wm0 + i * 32 + p * ROWS_PER_PASS + rr, col, M);
+      for (int p = 0; p < PASSES; ++p) {
+        const int r = p * ROWS_PER_PASS + rr;
+        if constexpr (kFold)
+          epi.finish_biased(fold4(v[p], rstat[wm0 + i * 32 + r], sfold, scol.b), cx[p], scol,
+                            m0 + wm0 + i * 32 + r, col, M);
+        else
+          epi.finish(v[p], cx[p], scol, m0 + wm0 + i * 32 + r, col, M);
+      }
     }
   };
   if (epi.row_loads(col_base, WCOLS))
@@ -364,7 +465,6 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
 // prepare(row, col, M, col_ctx): the row-dependent loads; blank(col_ctx): the context when there
 // are none; finish(v, ctx, col_ctx, row, col, M): the arithmetic and the stores.
 
-__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ float4 add4(const f32x4& v, const float4& b) {
   return float4{v[0] + b.x, v[1] + b.y, v[2] + b.z, v[3] + b.w};
 }
@@ -397,6 +497,7 @@ __device__ __forceinline__ void buffer_st_bf16x4(__amdgpu_buffer_rsrc_t r, uint3
 }
 
 struct EpiBiasF32Bf16 {
+  static constexpr bool kFoldable = false;
   const float* bias;
   float* out_f32;
   bf16* out_bf16;
@@ -418,6 +519,7 @@ struct EpiBiasF32Bf16 {
 };
 
 struct EpiBiasF32 {
+  static constexpr bool kFoldable = false;
   const float* bias;
   float* out;
   int ldo;
@@ -439,6 +541,7 @@ struct EpiBiasF32 {
 };
 
 struct EpiBiasF32RowMap {
+  static constexpr bool kFoldable = false;
   const float* bias;
   float* out;
   int ldo;
@@ -463,6 +566,7 @@ struct EpiBiasF32RowMap {
 };
 
 struct EpiBiasSiluBf16 {
+  static constexpr bool kFoldable = false;
   const float* bias;
   bf16* out;
   int ldo;
@@ -482,6 +586,7 @@ struct EpiBiasSiluBf16 {
 };
 
 struct EpiBiasGeluBf16 {
+  static constexpr bool kFoldable = true;  // FF1
   const float* bias;
   bf16* out;
   int ldo;
@@ -492,8 +597,12 @@ struct EpiBiasGeluBf16 {
   __device__ bool direct(int) const { return false; }
   __device__ Col column(int col) const { return {ld4(bias + col)}; }
   __device__ Ctx prepare(int, int, int, const Col&) const { return {}; }
-  __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
-    const float4 y = add4(v, c.b);
+  __device__ void finish(const f32x4& v, const Ctx& x, const Col& c, int row, int col, int M) const {
+    finish_biased(add4(v, c.b), x, c, row, col, M);
+  }
+  // y = acc + bias already (the LayerNorm fold adds the bias with its own terms)
+  __device__ void finish_biased(const float4& y, const Ctx&, const Col&, int row, int col,
+                                int M) const {
     const bf16x4 yb = {f2bf(gelu_tanh(y.x)), f2bf(gelu_tanh(y.y)), f2bf(gelu_tanh(y.z)),
                        f2bf(gelu_tanh(y.w))};
     buffer_st_bf16x4(buffer_over(out, (uint32_t)M * ldo * 2), (uint32_t)(row * ldo + col) * 2, yb);
@@ -503,15 +612,24 @@ struct EpiBiasGeluBf16 {
 // h += gate * (acc + bias).  kPerDoc: each document has its own gate row (gate + d * mod_stride,
 // d = docid[row]); otherwise one gate row is shared by every document and is loaded with the
 // bias, before the K loop.  h is read and written through raw buffer accesses over its M rows.
-template <bool kPerDoc>
+// kNext (shared gate rows only): also write the next LayerNorm fold's inputs for the new h:
+// anext = bf16(h * gnext) and, per row and 32-column chunk, (sum, centered sum of squares).
+// The 8 lanes holding a chunk's columns reduce it in a fixed order (sum8), so the statistics are
+// the same for every tile shape.
+template <bool kPerDoc, bool kNext>
 struct EpiGatedResidual {
+  static constexpr bool kFoldable = false;
   const float* bias;
   float* h;
   int ldh;
   const float* gate;  // mod + gate offset
   long mod_stride;
   const int32_t* docid;
-  struct Col { float4 b, g; };
+  const float* gnext;  // next LayerNorm's scale row
+  bf16* anext;         // [M][ldh]
+  float2* stats;       // [M][kStatChunks]
+  static_assert(!(kPerDoc && kNext), "the fold needs one modulation row for every document");
+  struct Col { float4 b, g, gn; };
   struct Ctx { float4 g, x; };
   __device__ bool row_loads(int, int) const { return true; }
   __device__ Ctx blank(const Col& c) const { return {c.g, float4{0.f, 0.f, 0.f, 0.f}}; }
@@ -520,6 +638,7 @@ struct EpiGatedResidual {
     Col c;
     c.b = ld4(bias + col);
     c.g = kPerDoc ? float4{0.f, 0.f, 0.f, 0.f} : ld4(gate + col);
+    c.gn = kNext ? ld4(gnext + col) : float4{0.f, 0.f, 0.f, 0.f};
     return c;
   }
   __device__ Ctx prepare(int row, int col, int M, const Col& c) const {
@@ -536,10 +655,22 @@ struct EpiGatedResidual {
     const float4 r = {x.x.x + x.g.x * y.x, x.x.y + x.g.y * y.y, x.x.z + x.g.z * y.z,
                       x.x.w + x.g.w * y.w};
     buffer_st4(buffer_over(h, (uint32_t)M * ldh * 4), (uint32_t)(row * ldh + col) * 4, r);
+    if constexpr (kNext) {
+      const bf16x4 a = {f2bf(r.x * c.gn.x), f2bf(r.y * c.gn.y), f2bf(r.z * c.gn.z),
+                        f2bf(r.w * c.gn.w)};
+      buffer_st_bf16x4(buffer_over(anext, (uint32_t)M * ldh * 2), (uint32_t)(row * ldh + col) * 2,
+                       a);
+      const float sum = sum8((r.x + r.y) + (r.z + r.w));
+      const float mc = sum * (1.0f / 32.0f);
+      const float d0 = r.x - mc, d1 = r.y - mc, d2 = r.z - mc, d3 = r.w - mc;
+      const float m2 = sum8((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3));
+      if ((threadIdx.x & 7) == 0 && row < M) stats[(long)row * kStatChunks + (col >> 5)] = float2{sum, m2};
+    }
   }
 };
 
 struct EpiQkvRope {
+  static constexpr bool kFoldable = true;
   const float* bias;
   int dim;        // heads * 64
   int rows;       // q / k row pitch per head (rp)
@@ -577,10 +708,14 @@ struct EpiQkvRope {
   }
   __device__ void finish(const f32x4& v, const Ctx& cx, const Col& cb, int row, int col,
                          int M) const {
+    finish_biased(add4(v, cb.b), cx, cb, row, col, M);
+  }
+  // y = acc + bias already (the LayerNorm fold adds the bias with its own terms)
+  __device__ void finish_biased(float4 y, const Ctx& cx, const Col&, int row, int col,
+                                int M) const {
     const int which = col / dim;  // 0 q, 1 k, 2 v
     const int c = col - which * dim;
     const int head = c >> 6, d = c & 63;
-    float4 y = add4(v, cb.b);
     if (which == 2) {
       // V transposed: vt[head][d + e][row]; rows in [M, rp) get finite copies of row M-1
       const bf16 v0 = f2bf(y.x), v1 = f2bf(y.y), v2 = f2bf(y.z), v3 = f2bf(y.w);
@@ -614,11 +749,21 @@ using Tile32x128 = TileCfg<32, 128, 1, 4>;
 
 template <class C, class Epi>
 hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
-                       const Epi& epi, hipStream_t stream, const int32_t* m_live) {
+                       const Epi& epi, hipStream_t stream, const int32_t* m_live,
+                       const FoldArgs& fold) {
   if (N % C::BN != 0 || K % C::BK != 0) return hipErrorInvalidValue;
   const int tiles = ((M + C::BM - 1) / C::BM) * (N / C::BN);
-  hipLaunchKernelGGL((gemm_kernel<C, Epi>), dim3(tiles), dim3(C::kThreads), 0, stream, A, lda, W,
-                     ldw, M, N, K, epi, m_live);
+  if constexpr (Epi::kFoldable) {
+    if (fold.u) {
+      hipLaunchKernelGGL((gemm_kernel<C, Epi, true>), dim3(tiles), dim3(C::kThreads), 0, stream,
+                         A, lda, W, ldw, M, N, K, epi, m_live, fold);
+      return hipGetLastError();
+    }
+  } else {
+    if (fold.u) return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL((gemm_kernel<C, Epi, false>), dim3(tiles), dim3(C::kThreads), 0, stream, A,
+                     lda, W, ldw, M, N, K, epi, m_live, fold);
   return hipGetLastError();
 }
 
@@ -654,19 +799,22 @@ inline int choose_tile(int M, int N) {
 // order, so a layout's results are the same under any capacity.
 template <class Epi>
 hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
-                  const Epi& epi, hipStream_t stream, const int32_t* m_live = nullptr) {
+                  const Epi& epi, hipStream_t stream, const int32_t* m_live = nullptr,
+                  const FoldArgs& fold = FoldArgs{nullptr, nullptr}) {
+  // the fold's statistics cover K = kStatChunks x 32 columns
+  if (fold.u && (!fold.stats || K != kStatChunks * 32)) return hipErrorInvalidValue;
   if (M <= 0) return hipSuccess;
   if (N % 128 != 0 || K % 64 != 0 || lda % 8 != 0 || ldw % 8 != 0) return hipErrorInvalidValue;
   // the copies address A and W by 32-bit byte offsets from their bases
   if ((long)M * lda * 2 >= (1L << 32) || (long)N * ldw * 2 >= (1L << 32)) return hipErrorInvalidValue;
   switch (choose_tile(M, N)) {
-    case 0: return launch_tile<Tile256x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
-    case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
-    case 2: return launch_tile<Tile128x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
-    case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
-    case 5: return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
-    case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
-    default: return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case 0: return launch_tile<Tile256x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+    case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+    case 2: return launch_tile<Tile128x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+    case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+    case 5: return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+    case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+    default: return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
   }
 }
 
@@ -709,32 +857,47 @@ hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, c
 
 hipError_t gemm_bias_gelu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, bf16* out, int ldo, hipStream_t stream,
-                               const int32_t* m_live) {
+                               const int32_t* m_live, const float* fold_u,
+                               const float2* fold_stats) {
   if ((long)M * ldo * 2 >= (1L << 31)) return hipErrorInvalidValue;  // buffer range is an int
-  return launch(A, lda, W, ldw, M, N, K, EpiBiasGeluBf16{bias, out, ldo}, stream, m_live);
+  return launch(A, lda, W, ldw, M, N, K, EpiBiasGeluBf16{bias, out, ldo}, stream, m_live,
+                FoldArgs{fold_stats, fold_u});
 }
 
 hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, float* h, int ldh, const float* gate,
                                long mod_stride, const int32_t* docid, hipStream_t stream,
-                               const int32_t* m_live) {
+                               const int32_t* m_live, const float* gnext, bf16* anext,
+                               float2* stats) {
   if ((long)M * ldh * 4 >= (1L << 31)) return hipErrorInvalidValue;  // buffer range is an int
+  if (gnext) {
+    if (mod_stride != 0 || !anext || !stats || N != kStatChunks * 32 || ldh % 4 != 0)
+      return hipErrorInvalidValue;
+    return launch(A, lda, W, ldw, M, N, K,
+                  EpiGatedResidual<false, true>{bias, h, ldh, gate, 0, docid, gnext, anext, stats},
+                  stream, m_live);
+  }
   if (mod_stride == 0)
     return launch(A, lda, W, ldw, M, N, K,
-                  EpiGatedResidual<false>{bias, h, ldh, gate, 0, docid}, stream, m_live);
+                  EpiGatedResidual<false, false>{bias, h, ldh, gate, 0, docid, nullptr, nullptr,
+                                                 nullptr},
+                  stream, m_live);
   return launch(A, lda, W, ldw, M, N, K,
-                EpiGatedResidual<true>{bias, h, ldh, gate, mod_stride, docid}, stream, m_live);
+                EpiGatedResidual<true, false>{bias, h, ldh, gate, mod_stride, docid, nullptr,
+                                              nullptr, nullptr},
+                stream, m_live);
 }
 
 hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const float* bias, int M,
                          int dim, int heads, const int32_t* pos, const float* rope_cos,
                          const float* rope_sin, int rope_dim, int max_pos, bf16* q, bf16* k,
-                         bf16* vt, int rp, hipStream_t stream, const int32_t* m_live) {
+                         bf16* vt, int rp, hipStream_t stream, const int32_t* m_live,
+                         const float* fold_u, const float2* fold_stats) {
   (void)heads;
   if (rp < M) return hipErrorInvalidValue;
   return launch(A, lda, W, ldw, M, 3 * dim, dim,
                 EpiQkvRope{bias, dim, rp, pos, rope_cos, rope_sin, rope_dim, max_pos, q, k, vt, rp},
-                stream, m_live);
+                stream, m_live, FoldArgs{fold_stats, fold_u});
 }
 
 }  // namespace fcv

@@ -1,5 +1,6 @@
 // Skinny products out[m, n] = f(sum_k W[n, k] a[m, k] + bias[n]) for rows of a that share
-// one W: the timestep MLP and the AdaLN projection, whose time is reading W (the concatenated
+// one W: the timestep MLP and the AdaLN projection (and, at the end of this file, the
+// LayerNorm fold's column terms), whose time is reading W (the concatenated
 // AdaLN weights are 137216 x 1024 bf16 = 281 MB per evaluation).  Bandwidth-bound, so no MFMA:
 // one wave owns 4 rows of W; lane l reads k in [8l, 8l + 8) of every 512-wide k block, so each
 // load instruction covers 1 KB of one W row contiguously.  A launch takes up to 16 rows of a,
@@ -107,7 +108,111 @@ hipError_t launch_gemv(const bf16* a, int lda, const bf16* W, int ldw, int M, in
   return hipErrorInvalidValue;
 }
 
+// ---- LayerNorm fold column terms (adaln_fold) ------------------------------------------
+// One wave per kFoldRows rows of W (a block's QKV rows, then its FF1 rows), converted to fp32
+// in registers; lane l holds k = 512 b + 8 l + 0..7.  For each modulation row the wave forms
+// 2 kFoldRows partial dot products (each row against g and against shift) and reduces them by
+// halving exchanges (xor 32, 16, 8, 4: a lane keeps half of its values, adds the partner's
+// copies of them, and hands over the other half), then a butterfly over the last 4 lanes:
+// lane 4 i ends with the full sum of value i.
+constexpr int kFoldRows = 8;
+constexpr int kFoldDim = 1024;
+
+template <int H>
+__device__ __forceinline__ void halve(float (&p)[2 * kFoldRows], bool upper, int mask) {
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const float send = upper ? p[i] : p[i + H];
+    const float keep = upper ? p[i + H] : p[i];
+    p[i] = keep + __shfl_xor(send, mask);
+  }
+}
+
+__global__ __launch_bounds__(256) void adaln_fold_kernel(
+    const bf16* __restrict__ qkv_w, const float* __restrict__ qkv_b, const bf16* __restrict__ ff1_w,
+    const float* __restrict__ ff1_b, int depth, int ff_dim, const float* __restrict__ mod,
+    long mod_width, int n_t, float* __restrict__ fold) {
+  constexpr int D = kFoldDim;
+  const int lane = threadIdx.x & 63;
+  const int waves_per_block = (3 * D + ff_dim) / kFoldRows;
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gw >= depth * waves_per_block) return;
+  const int l = gw / waves_per_block;
+  const int r0 = (gw - l * waves_per_block) * kFoldRows;  // row of [QKV rows | FF1 rows]
+  const bool att = r0 < 3 * D;
+  const int rf = r0 - 3 * D;
+  const bf16* W = att ? qkv_w + ((long)l * 3 * D + r0) * D : ff1_w + ((long)l * ff_dim + rf) * D;
+  const float* bias = att ? qkv_b + (long)l * 3 * D + r0 : ff1_b + (long)l * ff_dim + rf;
+  const long per_block = 6L * D + 2L * ff_dim;
+  const long u_off = att ? r0 : 6L * D + rf;
+  const long v_off = att ? 3L * D + r0 : 6L * D + ff_dim + rf;
+  const int g_off = att ? D : 4 * D, s_off = att ? 0 : 3 * D;
+
+  float w[kFoldRows][16];
+#pragma unroll
+  for (int r = 0; r < kFoldRows; ++r)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(W + (long)r * D + 512 * b + 8 * lane);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[r][8 * b + e] = bf2f(v[e]);
+    }
+  for (int s = 0; s < n_t; ++s) {
+    const float* mrow = mod + s * mod_width + (long)l * 6 * D;
+    float g[16], sh[16];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4 gv = *reinterpret_cast<const float4*>(mrow + g_off + 512 * b + 8 * lane + 4 * h);
+        const float4 sv = *reinterpret_cast<const float4*>(mrow + s_off + 512 * b + 8 * lane + 4 * h);
+        const int e = 8 * b + 4 * h;
+        g[e] = gv.x, g[e + 1] = gv.y, g[e + 2] = gv.z, g[e + 3] = gv.w;
+        sh[e] = sv.x, sh[e + 1] = sv.y, sh[e + 2] = sv.z, sh[e + 3] = sv.w;
+      }
+    float p[2 * kFoldRows];
+#pragma unroll
+    for (int r = 0; r < kFoldRows; ++r) {
+      float a = 0.0f, c = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        a = fmaf(w[r][e], g[e], a);
+        c = fmaf(w[r][e], sh[e], c);
+      }
+      p[2 * r] = a;
+      p[2 * r + 1] = c;
+    }
+    halve<8>(p, lane & 32, 32);
+    halve<4>(p, lane & 16, 16);
+    halve<2>(p, lane & 8, 8);
+    halve<1>(p, lane & 4, 4);
+    float t = p[0];
+    t += __shfl_xor(t, 2);
+    t += __shfl_xor(t, 1);
+    if ((lane & 3) == 0) {
+      const int vi = lane >> 2, r = vi >> 1;
+      float* out = fold + ((long)s * depth + l) * per_block;
+      if (vi & 1)
+        out[v_off + r] = t + bias[r];
+      else
+        out[u_off + r] = t;
+    }
+  }
+}
+
 }  // namespace
+
+hipError_t adaln_fold(const bf16* qkv_w, const float* qkv_b, const bf16* ff1_w,
+                      const float* ff1_b, int depth, int dim, int ff_dim, const float* mod,
+                      long mod_width, int n_t, float* fold, hipStream_t stream) {
+  if (dim != kFoldDim || ff_dim % kFoldRows != 0 || depth < 1 || n_t < 1 ||
+      mod_width < 6L * dim * depth || mod_width % 4 != 0)
+    return hipErrorInvalidValue;
+  const long waves = (long)depth * ((3 * dim + ff_dim) / kFoldRows);
+  hipLaunchKernelGGL(adaln_fold_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream,
+                     qkv_w, qkv_b, ff1_w, ff1_b, depth, ff_dim, mod, mod_width, n_t, fold);
+  return hipGetLastError();
+}
 
 bool gemv_supported(int M, int K, int lda, int ldw) {
   return M >= 1 && (K == 1024 || K == 512) && lda % 8 == 0 && ldw % 8 == 0;

@@ -16,6 +16,16 @@ namespace fcv {
 // Launchers given live == nullptr use their static count arguments.
 enum { kLiveRows = 0, kLiveTiles = 1, kLiveHalfRows = 2 };  // internal rows, attention tiles, rc
 
+// ---- LayerNorm folded into the next GEMM ----------------------------------------------
+// With one modulation row shared by every document, (LN(x) * g + shift) . W^T + bias is
+//   rs * (bf16(x * g) . W^T) - mu * rs * (W . g) + (W . shift + bias),
+// mu and rs = 1 / sqrt(var + 1e-6) the row's LayerNorm statistics.  The gated-residual GEMM
+// that produces x writes bf16(x * g) and, per row, kStatChunks chunks of 32 columns as
+// (sum, centered sum of squares); the next GEMM (fold_u = W . g, bias = W . shift + bias, both
+// from adaln_fold) combines the chunks in a fixed order.  Rows' statistics and products then
+// do not depend on the tile shape or on the batch.
+constexpr int kStatChunks = 32;  // the model width, 1024, in chunks of 32 columns
+
 // ---- GEMM: C[M,N] = A[M,K] . W[N,K]^T (+ bias) with a fused epilogue -------------------
 // Requirements checked by the caller: N % 128 == 0, K % 64 == 0, lda/ldw % 8 == 0.
 // M is the capacity the grid is sized for; m_live (when not null) holds the live row count
@@ -40,17 +50,22 @@ hipError_t gemm_bias_f32_rowmap(const bf16* A, int lda, const bf16* W, int ldw,
 hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, bf16* out, int ldo, hipStream_t stream);
 
-// out[r, c] = bf16(gelu_tanh(acc + bias[c]))   (FF1)
+// out[r, c] = bf16(gelu_tanh(acc + bias[c]))   (FF1).  With fold_u: the LayerNorm fold, acc
+// replaced by rs * acc - mu * rs * fold_u[c] from fold_stats (K must be kStatChunks * 32).
 hipError_t gemm_bias_gelu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, bf16* out, int ldo, hipStream_t stream,
-                               const int32_t* m_live = nullptr);
+                               const int32_t* m_live = nullptr, const float* fold_u = nullptr,
+                               const float2* fold_stats = nullptr);
 
 // h[r, c] += gate[c] * (acc + bias[c]), gate row = mod + docid[r] * mod_stride + gate_off
-// (out-projection and FF2 gated residuals)
+// (out-projection and FF2 gated residuals).  With gnext (mod_stride 0, N = kStatChunks * 32):
+// also anext[r, c] = bf16(h[r, c] * gnext[c]) and stats[r][chunk], the next LayerNorm fold's
+// inputs.
 hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, float* h, int ldh, const float* mod,
                                long mod_stride, const int32_t* docid, hipStream_t stream,
-                               const int32_t* m_live = nullptr);
+                               const int32_t* m_live = nullptr, const float* gnext = nullptr,
+                               bf16* anext = nullptr, float2* stats = nullptr);
 
 // Fused QKV projection: bias, interleaved RoPE on columns [0, rope_dim) of q and k
 // (angles from cos/sin tables [max_pos][rope_dim/2], row position min(pos[r], max_pos-1)),
@@ -58,7 +73,8 @@ hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, c
 hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const float* bias, int M,
                          int dim, int heads, const int32_t* pos, const float* rope_cos,
                          const float* rope_sin, int rope_dim, int max_pos, bf16* q, bf16* k,
-                         bf16* vt, int rp, hipStream_t stream, const int32_t* m_live = nullptr);
+                         bf16* vt, int rp, hipStream_t stream, const int32_t* m_live = nullptr,
+                         const float* fold_u = nullptr, const float2* fold_stats = nullptr);
 
 // ---- skinny products (few rows sharing W, K in {512, 1024}): bandwidth-bound, no MFMA -------
 // Launches of up to 16 rows each; a row's result is the same whatever M is.
@@ -66,6 +82,14 @@ bool gemv_supported(int M, int K, int lda, int ldw);
 // out[m, n] = acc + bias[n]
 hipError_t gemv_bias_f32(const bf16* a, int lda, const bf16* W, int ldw, const float* bias, int M,
                          int N, int K, float* out, int ldo, hipStream_t stream);
+// The LayerNorm fold's column terms for n_t modulation rows (row s at mod + s * mod_width) and
+// every block l < depth: fold + (s * depth + l) * (6 dim + 2 ff_dim) holds
+//   [W_qkv . g_att | W_qkv . shift_att + b_qkv | W_ff1 . g_ff | W_ff1 . shift_ff + b_ff1],
+// with (shift_att, g_att) at block offsets (0, dim) and (shift_ff, g_ff) at (3 dim, 4 dim) of
+// the block's 6 dim modulation columns.  fp32 dot products of the bf16 weights; dim 1024.
+hipError_t adaln_fold(const bf16* qkv_w, const float* qkv_b, const bf16* ff1_w,
+                      const float* ff1_b, int depth, int dim, int ff_dim, const float* mod,
+                      long mod_width, int n_t, float* fold, hipStream_t stream);
 // out[m, n] = bf16(silu(acc + bias[n]))
 hipError_t gemv_bias_silu_bf16(const bf16* a, int lda, const bf16* W, int ldw, const float* bias,
                                int M, int N, int K, bf16* out, int ldo, hipStream_t stream);
