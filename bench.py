@@ -451,7 +451,8 @@ def main() -> int:
                                       use_graph=graph, concurrency=concurrency)
 
     def probed_eager(stage: int, repeat: int = 1) -> tuple[list[float], float]:
-        """One eager K-step solve with HIP events around `stage` (block 0) every step; with
+        """One eager K-step solve with HIP events around `stage` (in block 1, whose launches
+        every later block repeats; the LN-modulate pass in block 0) every step; with
         repeat > 1 the probed launch runs `repeat` times back to back inside the pair and the
         library reports the per-launch time."""
         _lib.check(lib.fcv_dit_probe_arm(handle, stage, K, repeat))
@@ -472,7 +473,8 @@ def main() -> int:
     torch.cuda.synchronize()
 
     # timed region 1: the dominant kernel (QKV GEMM), HIP events on its stream, eager launches;
-    # each pair brackets QKV_REPEAT back-to-back launches of block 0's QKV GEMM
+    # each pair brackets QKV_REPEAT back-to-back launches of block 1's QKV GEMM (the LayerNorm
+    # folded into it, as in every block after the first)
     log(f"[bench] timing {K} steps eagerly with events around the QKV GEMM")
     qkv_ms, eager_wall = probed_eager(0, QKV_REPEAT)
     qkv_avg = sum(qkv_ms) / len(qkv_ms)
@@ -505,7 +507,7 @@ def main() -> int:
 
     breakdown = {}
     if not args.no_breakdown:
-        log("[bench] per-stage breakdown (eager, events around each stage in block 0)")
+        log("[bench] per-stage breakdown (eager, events around each stage in block 1)")
         for stage, name in enumerate(_lib.STAGES):
             accumulates = name in ("out_proj", "ff2", "euler", "forward")
             vals, _ = probed_eager(stage, 1 if accumulates else QKV_REPEAT)
@@ -572,9 +574,10 @@ def main() -> int:
         "mfma_util_pct": round(100 * mfma_util, 2),
         "tflops_per_step": round(flops["total"] / 1e12, 4),
         "roofline": {
-            "kernel": "qkv_gemm (fused bias + RoPE + head-major scatter), block 0, every step",
+            "kernel": ("qkv_gemm (folded LayerNorm + bias + RoPE + head-major scatter), "
+                       "block 1, every step"),
             "timing": (f"HIP events (no system fence) on the launch stream around {QKV_REPEAT} "
-                       "back-to-back launches of block 0's QKV GEMM, every step of an eager "
+                       "back-to-back launches of block 1's QKV GEMM, every step of an eager "
                        "K-step solve"),
             "bound": "mfma",
             "achieved": round(achieved, 1),

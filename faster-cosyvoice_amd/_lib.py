@@ -85,6 +85,12 @@ SIGNATURES = {
     "fcv_dit_solve": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                 POINTER(c_float), POINTER(c_float), c_int32, c_float, c_int32,
                                 c_void_p]),
+    "fcv_dit_schedule_bytes": (c_size_t, [c_void_p, c_int32]),
+    "fcv_dit_schedule": (c_int32, [c_void_p, POINTER(c_float), c_int32, c_void_p, c_size_t,
+                                   c_void_p]),
+    "fcv_dit_solve_scheduled": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                          POINTER(c_float), c_int32, c_float, c_void_p,
+                                          c_size_t, c_int32, c_void_p]),
     "fcv_pack_padded": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p,
                                   c_void_p]),
     "fcv_unpack_padded": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p,

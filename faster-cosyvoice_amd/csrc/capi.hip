@@ -159,17 +159,22 @@ struct FcvDit {
     probe_repeat = 1;
   }
 
-  // event pair around one launch of `stage` in block `layer` (-1 = outside the blocks)
+  // The probed launch of a stage: in block 1, the first whose LayerNorms fold into its GEMMs
+  // and so the launch every later block repeats (block 0 for a one-block model, and for the
+  // LN-modulate pass, which the fold leaves in block 0 only); layer -1 = outside the blocks.
+  bool probed(int stage, int layer) const {
+    if (stage != probe_stage || probe_count >= probe_pairs) return false;
+    const int target = (stage == FCV_STAGE_LN_MOD || dims.depth == 1) ? 0 : 1;
+    return layer < 0 || layer == target;
+  }
   hipError_t probe_begin(int stage, int layer, hipStream_t s) {
-    if (stage != probe_stage || layer > 0 || probe_count >= probe_pairs) return hipSuccess;
+    if (!probed(stage, layer)) return hipSuccess;
     return hipEventRecord(probe_events[2 * probe_count], s);
   }
   // launches of `stage` in block `layer` to issue: `probe_repeat` while that launch is probed
-  int launches(int stage, int layer) const {
-    return (stage == probe_stage && layer <= 0 && probe_count < probe_pairs) ? probe_repeat : 1;
-  }
+  int launches(int stage, int layer) const { return probed(stage, layer) ? probe_repeat : 1; }
   hipError_t probe_end(int stage, int layer, hipStream_t s) {
-    if (stage != probe_stage || layer > 0 || probe_count >= probe_pairs) return hipSuccess;
+    if (!probed(stage, layer)) return hipSuccess;
     return hipEventRecord(probe_events[2 * probe_count++ + 1], s);
   }
 };
@@ -177,17 +182,15 @@ struct FcvDit {
 namespace {
 
 // timestep embedding -> SiLU(temb) -> every block's AdaLN modulation in one projection, for
-// n_t time values: row i of the `mod` region (mod_width floats) belongs to t[i]
+// n_t time values (device t): row i of `mod` (mod_width floats) belongs to t[i]
 // (TimestepEmbedding modules.py:606-616; _project_modulations flashinfer_dit.py:430-445).
-// With `fold` (n_t <= kModGroup), also the LayerNorm fold's column terms of each row.
-int compute_modulations(FcvDit* m, const float* t, int n_t, bool fold, hipStream_t s) {
+// With `fold` (n_t <= kModGroup), also the LayerNorm fold's column terms of each row (row i at
+// fold + i * fold_width).  tsin / t1 / t2: scratch for n_t rows of 256 / dim / dim bf16.
+int modulation_rows(FcvDit* m, const float* t, int n_t, bf16* tsin, bf16* t1, bf16* t2,
+                    float* mod, float* fold, hipStream_t s) {
   const FcvDitWeights& w = m->w;
   const int D = m->dims.dim;
   auto B = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
-  float* mod = m->at<float>(m->L.mod);
-  bf16* tsin = m->at<bf16>(m->L.tsin);
-  bf16* t1 = m->at<bf16>(m->L.t1);
-  bf16* t2 = m->at<bf16>(m->L.t2);
   FCV_HIP(fcv::timestep_sinusoid(t, n_t, 256, tsin, s));
   FCV_HIP(fcv::gemm_bias_silu_bf16(tsin, 256, B(w.temb_w1), 256, w.temb_b1, n_t, D, 256, t1, D, s));
   FCV_HIP(fcv::gemm_bias_silu_bf16(t1, D, B(w.temb_w2), D, w.temb_b2, n_t, D, D, t2, D, s));
@@ -197,9 +200,40 @@ int compute_modulations(FcvDit* m, const float* t, int n_t, bool fold, hipStream
                                (int)m->mod_width, (int)m->mod_width, s));
   if (fold)
     FCV_HIP(fcv::adaln_fold(B(w.qkv_w), w.qkv_b, B(w.ff1_w), w.ff1_b, m->dims.depth, D,
-                            m->dims.ff_dim, mod, m->mod_width, n_t, m->at<float>(m->L.fold), s));
+                            m->dims.ff_dim, mod, m->mod_width, n_t, fold, s));
   FCV_HIP(m->probe_end(FCV_STAGE_ADALN, -1, s));
   return FCV_OK;
+}
+
+// modulation_rows into the workspace's mod (and fold) region
+int compute_modulations(FcvDit* m, const float* t, int n_t, bool fold, hipStream_t s) {
+  return modulation_rows(m, t, n_t, m->at<bf16>(m->L.tsin), m->at<bf16>(m->L.t1),
+                         m->at<bf16>(m->L.t2), m->at<float>(m->L.mod),
+                         fold ? m->at<float>(m->L.fold) : nullptr, s);
+}
+
+// A solve schedule (fcv_dit_schedule): device t values, scratch for one group of kModGroup
+// time rows, then every step's modulation row and fold terms.
+struct Schedule {
+  size_t t, tsin, t1, t2, mod, fold, total;
+};
+Schedule schedule_layout(const FcvDitDims& d, long n_steps) {
+  Schedule S{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off = align_up(off + bytes, kAlign);
+    return at;
+  };
+  const long mod_width = (long)d.depth * 6 * d.dim + 2L * d.dim;
+  S.t = take(kMaxSteps * 4);
+  S.tsin = take(kModGroup * 256 * 2);
+  S.t1 = take((long)kModGroup * d.dim * 2);
+  S.t2 = take((long)kModGroup * d.dim * 2);
+  S.mod = take(n_steps * mod_width * 4);
+  S.fold = take(n_steps * fold_width(d) * 4);
+  S.total = off;
+  return S;
 }
 
 int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
@@ -554,33 +588,39 @@ int fcv_euler_cfg_step(FcvDit* m, float* x, const float* v, float dt, float cfg,
   return FCV_OK;
 }
 
-int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const float* spks,
-                  const float* t_host, const float* dt_host, int32_t n_steps, float cfg,
-                  int32_t use_graph, hipStream_t s) {
-  FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
-  FCV_CHECK(m->planned, FCV_ERR_STATE, "fcv_dit_solve called before fcv_dit_plan");
-  FCV_CHECK(x && mu && cond && spks && t_host && dt_host, FCV_ERR_INVALID, "null argument");
-  FCV_CHECK(n_steps >= 1 && n_steps <= kMaxSteps, FCV_ERR_INVALID, "n_steps must be in [1, 64]");
+}  // extern "C"
+
+namespace {
+
+// The CFG Euler loop of fcv_dit_solve (sched == nullptr: the modulation rows are computed in
+// the loop, kModGroup steps per pass over the AdaLN weights) and of fcv_dit_solve_scheduled
+// (sched: a schedule buffer holding every step's rows).
+int solve_loop(FcvDit* m, float* x, const float* mu, const float* cond, const float* spks,
+               const float* t_host, const float* dt_host, int32_t n_steps, float cfg,
+               const char* sched, int32_t use_graph, hipStream_t s) {
   int rc = check_cfg_layout(m);
   if (rc != FCV_OK) return rc;
 
   float* tbuf = m->at<float>(m->L.tbuf);
   float* vbuf = m->at<float>(m->L.vbuf);
   const int mel = m->dims.mel_dim;
-  FCV_HIP(hipMemcpyAsync(tbuf, t_host, n_steps * sizeof(float), hipMemcpyHostToDevice, s));
+  const Schedule S = schedule_layout(m->dims, n_steps);
+  if (!sched)
+    FCV_HIP(hipMemcpyAsync(tbuf, t_host, n_steps * sizeof(float), hipMemcpyHostToDevice, s));
 
   auto body = [&]() -> int {
     m->probe_count = 0;
-    const float* mod = m->at<float>(m->L.mod);
-    const float* fold = m->at<float>(m->L.fold);
+    const float* mod = sched ? reinterpret_cast<const float*>(sched + S.mod) : m->at<float>(m->L.mod);
+    const float* fold =
+        sched ? reinterpret_cast<const float*>(sched + S.fold) : m->at<float>(m->L.fold);
     for (int step = 0; step < n_steps; ++step) {
       // every kModGroup steps, one pass over the AdaLN weights gives the next steps' rows
-      if (step % kModGroup == 0) {
+      if (!sched && step % kModGroup == 0) {
         int r = compute_modulations(m, tbuf + step, std::min(kModGroup, n_steps - step), true,
                                     s);
         if (r != FCV_OK) return r;
       }
-      const int row = step % kModGroup;
+      const int row = sched ? step : step % kModGroup;
       int r = run_forward(m, x, mu, cond, spks, nullptr, 1, mod + row * m->mod_width,
                           fold + row * fold_width(m->dims), vbuf, s);
       if (r != FCV_OK) return r;
@@ -592,12 +632,13 @@ int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const
     return FCV_OK;
   };
   // What a captured loop bakes in: the capacity (workspace offsets and grids), the mask, the
-  // workspace and solver buffers, and the schedule (t is read from tbuf).  The layout itself is
-  // read from the workspace at run time, so any layout planned into the same capacity replays.
+  // workspace and solver buffers, the schedule buffer, and the schedule (t is read from tbuf or
+  // the schedule buffer).  The layout itself is read from the workspace at run time, so any
+  // layout planned into the same capacity replays.
   std::vector<uintptr_t> key = {(uintptr_t)m->rows_cap, (uintptr_t)m->docs_cap,
                                 (uintptr_t)m->mask_mode, (uintptr_t)m->chunk, (uintptr_t)m->ws,
                                 (uintptr_t)x, (uintptr_t)mu, (uintptr_t)cond, (uintptr_t)spks,
-                                (uintptr_t)n_steps};
+                                (uintptr_t)sched, (uintptr_t)n_steps};
   uint32_t bits;
   std::memcpy(&bits, &cfg, 4);
   key.push_back(bits);
@@ -644,6 +685,62 @@ int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const
   }
   FCV_HIP(hipGraphLaunch(m->graphs.front().exec, s));
   return FCV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fcv_dit_solve(FcvDit* m, float* x, const float* mu, const float* cond, const float* spks,
+                  const float* t_host, const float* dt_host, int32_t n_steps, float cfg,
+                  int32_t use_graph, hipStream_t s) {
+  FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
+  FCV_CHECK(m->planned, FCV_ERR_STATE, "fcv_dit_solve called before fcv_dit_plan");
+  FCV_CHECK(x && mu && cond && spks && t_host && dt_host, FCV_ERR_INVALID, "null argument");
+  FCV_CHECK(n_steps >= 1 && n_steps <= kMaxSteps, FCV_ERR_INVALID, "n_steps must be in [1, 64]");
+  return solve_loop(m, x, mu, cond, spks, t_host, dt_host, n_steps, cfg, nullptr, use_graph, s);
+}
+
+size_t fcv_dit_schedule_bytes(const FcvDit* m, int32_t n_steps) {
+  if (!m || n_steps < 1 || n_steps > kMaxSteps) return 0;
+  return schedule_layout(m->dims, n_steps).total;
+}
+
+int fcv_dit_schedule(FcvDit* m, const float* t_host, int32_t n_steps, void* sched,
+                     size_t sched_bytes, hipStream_t s) {
+  FCV_CHECK(m && t_host && sched, FCV_ERR_INVALID, "null argument");
+  FCV_CHECK(n_steps >= 1 && n_steps <= kMaxSteps, FCV_ERR_INVALID, "n_steps must be in [1, 64]");
+  FCV_CHECK(((uintptr_t)sched) % kAlign == 0, FCV_ERR_INVALID,
+            "schedule buffer must be 256-byte aligned");
+  const Schedule S = schedule_layout(m->dims, n_steps);
+  FCV_CHECK(sched_bytes >= S.total, FCV_ERR_INVALID, "schedule buffer too small");
+  char* b = static_cast<char*>(sched);
+  float* t = reinterpret_cast<float*>(b + S.t);
+  FCV_HIP(hipMemcpyAsync(t, t_host, n_steps * sizeof(float), hipMemcpyHostToDevice, s));
+  const long fw = fold_width(m->dims);
+  for (int step = 0; step < n_steps; step += kModGroup) {
+    int r = modulation_rows(m, t + step, std::min(kModGroup, n_steps - step),
+                            reinterpret_cast<bf16*>(b + S.tsin), reinterpret_cast<bf16*>(b + S.t1),
+                            reinterpret_cast<bf16*>(b + S.t2),
+                            reinterpret_cast<float*>(b + S.mod) + step * m->mod_width,
+                            reinterpret_cast<float*>(b + S.fold) + step * fw, s);
+    if (r != FCV_OK) return r;
+  }
+  return FCV_OK;
+}
+
+int fcv_dit_solve_scheduled(FcvDit* m, float* x, const float* mu, const float* cond,
+                            const float* spks, const float* dt_host, int32_t n_steps, float cfg,
+                            const void* sched, size_t sched_bytes, int32_t use_graph,
+                            hipStream_t s) {
+  FCV_CHECK(m, FCV_ERR_INVALID, "null handle");
+  FCV_CHECK(m->planned, FCV_ERR_STATE, "fcv_dit_solve_scheduled called before fcv_dit_plan");
+  FCV_CHECK(x && mu && cond && spks && dt_host && sched, FCV_ERR_INVALID, "null argument");
+  FCV_CHECK(n_steps >= 1 && n_steps <= kMaxSteps, FCV_ERR_INVALID, "n_steps must be in [1, 64]");
+  FCV_CHECK(sched_bytes >= schedule_layout(m->dims, n_steps).total, FCV_ERR_INVALID,
+            "schedule buffer too small for n_steps");
+  return solve_loop(m, x, mu, cond, spks, nullptr, dt_host, n_steps, cfg,
+                    static_cast<const char*>(sched), use_graph, s);
 }
 
 int fcv_pack_padded(FcvDit* m, const float* src, int32_t batch, int32_t channels,

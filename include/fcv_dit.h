@@ -133,6 +133,26 @@ int fcv_dit_solve(FcvDit* dit, float* x, const float* mu, const float* cond, con
                   const float* t_host, const float* dt_host, int32_t n_steps, float cfg,
                   int32_t use_graph, hipStream_t stream);
 
+/* A solve schedule shared by handles: the modulation rows of an n_steps Euler schedule (every
+ * block's AdaLN shift/scale/gate and the final (scale, shift), _project_modulations
+ * flashinfer_dit.py:430-445, plus the LayerNorm fold's column terms) for t_host[0..n_steps),
+ * computed once by fcv_dit_schedule into a caller buffer of fcv_dit_schedule_bytes(dit,
+ * n_steps) bytes (256-byte aligned; 0 for an invalid n_steps).  fcv_dit_solve_scheduled is
+ * fcv_dit_solve reading its modulation rows from that buffer instead of computing them: the
+ * request groups of one solve, each on its own handle and stream over the same weights, pass
+ * one buffer and pay for one pass over the AdaLN weights instead of one per group (the
+ * reference's single packed batch computes them once, flashinfer_flow.py:16-74).  The buffer
+ * must come from a handle over the same weights, hold at least n_steps steps, and stay intact
+ * until every solve reading it has finished; its pointer is part of the captured graph's key.
+ * Results are bit-identical to fcv_dit_solve with the same t_host. */
+size_t fcv_dit_schedule_bytes(const FcvDit* dit, int32_t n_steps);
+int fcv_dit_schedule(FcvDit* dit, const float* t_host, int32_t n_steps, void* schedule,
+                     size_t schedule_bytes, hipStream_t stream);
+int fcv_dit_solve_scheduled(FcvDit* dit, float* x, const float* mu, const float* cond,
+                            const float* spks, const float* dt_host, int32_t n_steps, float cfg,
+                            const void* schedule, size_t schedule_bytes, int32_t use_graph,
+                            hipStream_t stream);
+
 /* Padded channel-first [batch][channels][padded_len] <-> packed rows [rows][channels] for the
  * planned layout (document b = batch row b), used by the drop-in padded estimator call
  * (flashinfer_dit.py:469-471 gather, :536-543 scatter into zeros). */
@@ -153,8 +173,10 @@ int fcv_dit_plan_info(const FcvDit* dit, int32_t* rows, int32_t* n_docs, int32_t
  * plan_calls counter, flashinfer_attention.py:61-62); it lets a benchmark time one kernel live
  * inside a solve.  Arms a probe on `stage`: during every later forward/solve call the library
  * records a HIP event pair (timing-only events, no system-scope fence) around that stage's
- * launch in block 0 (or its one launch for stages outside the blocks), for the first n_pairs
- * launches counted from the start of the call.  With repeat > 1 the probed launch is issued
+ * launch in block 1 (the first block whose LayerNorms fold into its GEMMs, whose launches every
+ * later block repeats; block 0 for a one-block model and for the LN-modulate stage), or around
+ * its one launch for stages outside the blocks, for the first n_pairs launches counted from the
+ * start of the call.  With repeat > 1 the probed launch is issued
  * `repeat` times back to back between the two events, so per-launch event overhead is
  * amortised; only stages whose launch is idempotent accept repeat > 1 (QKV, attention, FF1,
  * LN-modulate, conv, AdaLN, input and output projections).  n_pairs == 0 disarms.  Arming or

@@ -240,6 +240,35 @@ def test_solve_twenty_steps_equals_stepwise(fcv, stress2):
         assert torch.equal(got, want), graph
 
 
+def test_shared_schedule_twenty_steps(fcv, stress2):
+    """The solve schedule shared by request groups (fcv_dit_schedule, then
+    fcv_dit_solve_scheduled on each group's handle): 20 steps, so the schedule holds rows past
+    one 16-row pass of the skinny product.  Two and three groups give bit for bit the sample of
+    one group solving with its own modulation rows (fcv_dit_solve), eagerly, on the first
+    capture and on a replay; a schedule buffer too small for the step count is refused."""
+    _, est = stress2
+    b = fcv.synthetic.make_batch("sched20", [70, 33, 41, 90], [20, 10, 15, 30], seed=62)
+    solve = lambda c, graph: fcv.solve_euler_packed(
+        est, b.noise, b.mu, b.cond, b.spks, b.lengths, n_steps=20, use_graph=graph,
+        concurrency=c).cpu()
+    ref = solve(1, False)
+    for c in (2, 3):
+        for graph in (False, True, True):
+            say(f"[sched20] groups={c} graph={graph}")
+            assert torch.equal(solve(c, graph), ref), (c, graph)
+    lib = fcv._lib.load()
+    handle = est._require()
+    small = lib.fcv_dit_schedule_bytes(handle, 10)
+    assert 0 < small < lib.fcv_dit_schedule_bytes(handle, 20)
+    assert lib.fcv_dit_schedule_bytes(handle, 65) == 0
+    buf = torch.empty(small, dtype=torch.uint8, device="cuda:0")
+    ts, dts = fcv.euler_schedule(20)
+    t_arr = (fcv._lib.c_float * 20)(*ts)
+    rc_code = lib.fcv_dit_schedule(handle, t_arr, 20, buf.data_ptr(), buf.numel(),
+                                   torch.cuda.current_stream().cuda_stream)
+    assert rc_code == fcv._lib.FCV_ERR_INVALID
+
+
 @pytest.mark.parametrize("streaming", [False, True])
 def test_peaked_attention_depth22(fcv, sharp22, streaming):
     """22 blocks on the peaked-attention recipe (q/k weights of deviation 0.05, gates +0.2):
