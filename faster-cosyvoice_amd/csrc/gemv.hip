@@ -5,7 +5,7 @@
 // one wave owns 4 rows of W; lane l reads k in [8l, 8l + 8) of every 512-wide k block, so each
 // load instruction covers 1 KB of one W row contiguously.  A launch takes up to 16 rows of a,
 // in chunks of up to 4 against the W rows held in registers; each chunk's 4 x 4 partial sums
-// are reduced with cross-lane shuffles and written by lane 0.  More rows take more launches of
+// are reduced together across the wave (reduce16) and written by the lanes holding them.  More rows take more launches of
 // 16.  Every output element is summed in the same order whatever M is, so a row's result does
 // not depend on how many rows share the call (one shared t, one t per document, or the t
 // values of a solver's steps all give a t the same modulation row, bit for bit).
@@ -32,6 +32,30 @@ struct GemvSiluBf16 {
     out[(long)m * ldo + n] = f2bf(silu(s + bias[n]));
   }
 };
+
+// Wave sums of 16 values at once: halving exchanges (xor 32, 16, 8, 4: a lane keeps half of its
+// values, adds the partner's copies of them and hands over the other half), then a butterfly
+// over the last 4 lanes; lane 4 j returns the full sum of value j (15 + 2 exchanges instead of
+// 16 x 6).
+template <int H>
+__device__ __forceinline__ void halve(float (&p)[16], bool upper, int mask) {
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const float send = upper ? p[i] : p[i + H];
+    const float keep = upper ? p[i + H] : p[i];
+    p[i] = keep + __shfl_xor(send, mask);
+  }
+}
+__device__ __forceinline__ float reduce16(float (&p)[16], int lane) {
+  halve<8>(p, lane & 32, 32);
+  halve<4>(p, lane & 16, 16);
+  halve<2>(p, lane & 8, 8);
+  halve<1>(p, lane & 4, 4);
+  float t = p[0];
+  t += __shfl_xor(t, 2);
+  t += __shfl_xor(t, 1);
+  return t;
+}
 
 // K % 512 == 0: lane l holds k = 512 b + 8 l + 0..7 for each of the K / 512 blocks b.  MM rows
 // of a per chunk; ceil(M / MM) chunks.
@@ -62,7 +86,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const bf16* __restrict__ a, i
 #pragma unroll
         for (int e = 0; e < 8; ++e) av[m][b][e] = bf2f(v[e]);
       }
-    float acc[kGemvRows][MM];
+    // partial sums, value v = r * MM + m, padded to 16 values
+    float p[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) p[v] = 0.0f;
 #pragma unroll
     for (int r = 0; r < kGemvRows; ++r)
 #pragma unroll
@@ -72,15 +99,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(const bf16* __restrict__ a, i
         for (int b = 0; b < KB; ++b)
 #pragma unroll
           for (int e = 0; e < 8; ++e) s = fmaf(bf2f(wv[r][b][e]), av[m][b][e], s);
-        acc[r][m] = wave_sum(s);
+        p[r * MM + m] = s;
       }
-    if (lane == 0) {
-#pragma unroll
-      for (int r = 0; r < kGemvRows; ++r)
-#pragma unroll
-        for (int m = 0; m < MM; ++m)
-          if (m0 + m < M && n0 + r < N) epi(m0 + m, n0 + r, acc[r][m]);
-    }
+    // lane 4 j ends with the full sum of value j
+    const float t = reduce16(p, lane);
+    const int v = lane >> 2, r = v / MM, m = v % MM;
+    if ((lane & 3) == 0 && v < kGemvRows * MM && m0 + m < M && n0 + r < N) epi(m0 + m, n0 + r, t);
   }
 }
 
@@ -110,23 +134,13 @@ hipError_t launch_gemv(const bf16* a, int lda, const bf16* W, int ldw, int M, in
 
 // ---- LayerNorm fold column terms (adaln_fold) ------------------------------------------
 // One wave per kFoldRows rows of W (a block's QKV rows, then its FF1 rows), converted to fp32
-// in registers; lane l holds k = 512 b + 8 l + 0..7.  For each modulation row the wave forms
-// 2 kFoldRows partial dot products (each row against g and against shift) and reduces them by
-// halving exchanges (xor 32, 16, 8, 4: a lane keeps half of its values, adds the partner's
-// copies of them, and hands over the other half), then a butterfly over the last 4 lanes:
-// lane 4 i ends with the full sum of value i.
+// in registers; lane l holds k = 512 b + 8 l + 0..7.  For each modulation row a wave forms
+// 2 kFoldRows partial dot products (each W row against g and against shift) and reduces them
+// together (reduce16): lane 4 i ends with the full sum of value i.  (Staging the g and shift
+// rows in LDS once per workgroup measured slower: 166 against 135 us for 10 rows.)
 constexpr int kFoldRows = 8;
 constexpr int kFoldDim = 1024;
-
-template <int H>
-__device__ __forceinline__ void halve(float (&p)[2 * kFoldRows], bool upper, int mask) {
-#pragma unroll
-  for (int i = 0; i < H; ++i) {
-    const float send = upper ? p[i] : p[i + H];
-    const float keep = upper ? p[i + H] : p[i];
-    p[i] = keep + __shfl_xor(send, mask);
-  }
-}
+static_assert(2 * kFoldRows == 16, "reduce16 takes 16 values");
 
 __global__ __launch_bounds__(256) void adaln_fold_kernel(
     const bf16* __restrict__ qkv_w, const float* __restrict__ qkv_b, const bf16* __restrict__ ff1_w,
@@ -182,13 +196,7 @@ __global__ __launch_bounds__(256) void adaln_fold_kernel(
       p[2 * r] = a;
       p[2 * r + 1] = c;
     }
-    halve<8>(p, lane & 32, 32);
-    halve<4>(p, lane & 16, 16);
-    halve<2>(p, lane & 8, 8);
-    halve<1>(p, lane & 4, 4);
-    float t = p[0];
-    t += __shfl_xor(t, 2);
-    t += __shfl_xor(t, 1);
+    const float t = reduce16(p, lane);
     if ((lane & 3) == 0) {
       const int vi = lane >> 2, r = vi >> 1;
       float* out = fold + ((long)s * depth + l) * per_block;
