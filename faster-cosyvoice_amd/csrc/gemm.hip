@@ -5,7 +5,8 @@
 // the bf16 peak in a register loop, the 16x16x32 form ~54%).
 //
 // Main loop.  A workgroup of WM x WN waves owns a BM x BN tile (256x256, 192x256, 128x256 and
-// 256x128 with 8 waves, 160x256, 128x128 and 32x128 with 4 waves, several workgroups per CU);
+// 256x128 with 8 waves, 160x256, 128x128, 96x128 and 32x128 with 4 waves, several workgroups
+// per CU);
 // each wave a sub-tile of 32x32 MFMA tiles.  Operands go straight from global memory into LDS
 // with global_load_lds_dwordx4 (no register staging, no ds_write; scalar base and LDS address,
 // per-lane 32-bit offset) through a ring of slices (by default two stages of K = 64: one
@@ -746,6 +747,7 @@ using Tile128x256 = TileCfg<128, 256, 2, 4>;
 using Tile256x128 = TileCfg<256, 128, 4, 2>;
 using Tile128x128 = TileCfg<128, 128, 2, 2>;
 using Tile32x128 = TileCfg<32, 128, 1, 4>;
+using Tile96x128 = TileCfg<96, 128, 1, 4>;
 
 template <class C, class Epi>
 hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
@@ -772,20 +774,24 @@ hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, in
 // (N = 1024, 2048, 3072 at ~4.6k and ~9.2k rows, production epilogues): 128x128 runs two
 // workgroups per CU, which its rate includes; 160x256 runs one wave per SIMD, so it rates low
 // although it fills more CUs; 32x128 is rated low so it only wins when the larger shapes leave
-// most CUs idle, as for the 128-column output projection.  The choice only changes which rows
+// most CUs idle, as for the 128-column output projection.  96x128 (four 96x32 waves, two
+// workgroups per CU) is only offered for the 1024-column GEMMs (out-projection, FF2), where it
+// was measured fastest from ~2k to ~6k rows (a request group's share of a batch): its rate puts
+// it between 32x128 below and 192x256 above.  The choice only changes which rows
 // and columns share a workgroup: every output element still accumulates its K slices in the
 // same order, so results are bitwise identical for every tile shape (batch invariance holds).
 constexpr int kCus = 256;
-constexpr int kTileShape[7][2] = {{256, 256}, {192, 256}, {128, 256}, {256, 128}, {128, 128},
-                                   {32, 128}, {160, 256}};
-constexpr float kTileRate[7] = {1.0f, 0.97f, 0.80f, 0.78f, 0.85f, 0.45f, 0.75f};
+constexpr int kTileShapes = 8;
+constexpr int kTileShape[kTileShapes][2] = {{256, 256}, {192, 256}, {128, 256}, {256, 128},
+                                            {128, 128}, {32, 128},  {160, 256}, {96, 128}};
+constexpr float kTileRate[kTileShapes] = {1.0f, 0.97f, 0.80f, 0.78f, 0.85f, 0.45f, 0.75f, 0.66f};
 
 inline int choose_tile(int M, int N) {
   int best = 4;
   float best_t = 3.0e38f;
-  for (int c = 0; c < 7; ++c) {
+  for (int c = 0; c < kTileShapes; ++c) {
     const int bm = kTileShape[c][0], bn = kTileShape[c][1];
-    if (N % bn != 0) continue;
+    if (N % bn != 0 || (c == 7 && N != 1024)) continue;
     const long tiles = (long)((M + bm - 1) / bm) * (N / bn);
     const long per_cu = (tiles + kCus - 1) / kCus;
     const float t = (float)per_cu * bm * bn / kTileRate[c];
@@ -814,6 +820,7 @@ hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, 
     case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     case 5: return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+    case 7: return launch_tile<Tile96x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     default: return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
   }
 }
