@@ -193,6 +193,32 @@ def test_shared_t_equals_per_doc_t(fcv, stress2):
         assert rel_l2(alone, full[cu[d]:cu[d + 1]]) < BF16_W_TOL, d
 
 
+def test_folded_layernorm_with_offset_residual(fcv):
+    """The folded LayerNorm rounds bf16(h * scale) instead of the normalized row, so its error
+    grows with the row mean relative to the spread.  With +3 on every input-projection bias
+    (the residual stream then carries a large mean) the folded path (one shared t) stays within
+    the velocity bound of the fp32 oracle; a bf16 emulation of both paths on the CPU puts it at
+    4.5e-3 against the bf16-weight oracle where the LN-pass path (the same t per document) is
+    at 3.5e-3 (3.0e-3 both without the offset).  The LN-pass path keeps the bf16-weight
+    bound."""
+    dims = fcv.synthetic.DiTDims(depth=2)
+    sd = fcv.synthetic.random_state_dict(dims, seed=21, gate_bias=0.5)
+    sd["input_embed.proj.bias"] = sd["input_embed.proj.bias"] + 3.0
+    est = make_estimator(fcv, sd, depth=2)
+    lengths = [200, 75, 31]
+    x, mu, cond, spks, t = random_packed(lengths, seed=29)
+    t = t[:1]
+    ref32 = oracle_packed(sd, x, mu, cond, spks, t, lengths)
+    ref16 = oracle_packed(bf16_weights(sd), x, mu, cond, spks, t, lengths)
+    folded = est.forward_packed(x, mu, cond, spks, t, lengths).cpu()
+    ln_pass = est.forward_packed(x, mu, cond, spks, t.expand(len(lengths)).clone(), lengths).cpu()
+    say(f"[offset_residual] vs fp32 oracle: folded {rel_l2(folded, ref32):.2e}, LN pass "
+        f"{rel_l2(ln_pass, ref32):.2e}; vs bf16-weight oracle: folded {rel_l2(folded, ref16):.2e}, "
+        f"LN pass {rel_l2(ln_pass, ref16):.2e}")
+    assert rel_l2(folded, ref32) <= VEL_TOL
+    assert rel_l2(ln_pass, ref16) <= BF16_W_TOL
+
+
 def test_padded_dropin_collapses_equal_t(fcv, stress2):
     """The padded drop-in gets t of length 2B, all equal, from the packed solver
     (flashinfer_flow.py:53-57); it computes one modulation row and gives the rows of the
