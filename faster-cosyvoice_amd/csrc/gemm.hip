@@ -177,6 +177,14 @@ __device__ __forceinline__ float4 fold4(const f32x4& v, float2 a, const float4& 
                 fmaf(a.x, v[2], fmaf(a.y, u.z, b.z)), fmaf(a.x, v[3], fmaf(a.y, u.w, b.w))};
 }
 
+// Whether an epilogue's per-row loads are issued one 32-row block ahead (the default); an
+// epilogue sets kPipelineRows = false when two blocks of its row context do not fit in registers.
+template <class E, class = void>
+struct pipeline_rows : std::true_type {};
+template <class E>
+struct pipeline_rows<E, std::void_t<decltype(E::kPipelineRows)>>
+    : std::bool_constant<E::kPipelineRows> {};
+
 template <class C, class Epi, bool kFold>
 __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
     const bf16* __restrict__ A, int lda, const bf16* __restrict__ W, int ldw, int M, int N, int K,
@@ -203,6 +211,14 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   // fold: the tile's rows' chunk statistics (rows past M take row M - 1's, as the A copies do),
   // fetched ahead of the operand copies so the wait for the first slice covers them; a pass
   // reads kStatRows consecutive rows as one contiguous span
+  // per-row epilogue inputs (row_info) of the tile's rows, fetched with the statistics and
+  // parked in LDS with the first slice
+  static_assert(BM <= C::kThreads, "one thread per tile row");
+  __shared__ int32_t rinfo[Epi::kRowInfo ? BM : 1];
+  int rin = -1;
+  if constexpr (Epi::kRowInfo) {
+    if ((int)threadIdx.x < BM && m0 + (int)threadIdx.x < M) rin = epi.row_info(m0 + threadIdx.x);
+  }
   float4 stat_in[kStatPasses];
   if constexpr (kFold) {
 #pragma unroll
@@ -342,6 +358,9 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
       if ((threadIdx.x & 15) == 0 && r < BM) rstat[r] = a;
     }
   }
+  if constexpr (Epi::kRowInfo) {
+    if ((int)threadIdx.x < BM) rinfo[threadIdx.x] = rin;
+  }
   __syncthreads();
   if (S - 1 < KT) issue(S - 1, S - 1);
   load(0, 0, 0);
@@ -414,11 +433,25 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   constexpr int PASSES = 32 / ROWS_PER_PASS;
   const int rr = lane / LANES_PER_ROW;
   const int col = col_base + rc;
-  // Two instantiations: tiles whose epilogue reads per-row data wait once per 32-row block,
-  // after issuing that block's loads (the wait also covers the previous block's stores: loads
-  // and stores share one counter); tiles without row data never wait.
+  // Two instantiations: tiles whose epilogue reads per-row data (the residual, rotary angles)
+  // issue each 32-row block's loads one block ahead, before the previous block's stores, so a
+  // block's wait covers loads that have been in flight for a whole block and not the stores
+  // just issued (loads and stores share one counter and complete in order); the rows' row_info
+  // comes from LDS, so no load waits on another.  Tiles without row data never wait.
+  auto prepare_block = [&](int i, Ctx (&cx)[PASSES]) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int tr = wm0 + i * 32 + p * ROWS_PER_PASS + rr;
+      int info = -1;
+      if constexpr (Epi::kRowInfo) info = rinfo[tr];
+      cx[p] = epi.prepare(m0 + tr, col, M, scol, info);
+    }
+  };
   auto staged = [&](auto loads_c) {
     constexpr bool kLoads = decltype(loads_c)::value;
+    constexpr bool kAhead = pipeline_rows<Epi>::value;
+    Ctx cx[PASSES];
+    if constexpr (kLoads && kAhead) prepare_block(0, cx);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -432,25 +465,36 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       f32x4 v[PASSES];
-      Ctx cx[PASSES];
 #pragma unroll
-      for (int p = 0; p < PASSES; ++p) {
-        const int r = p * ROWS_PER_PASS + rr;
-        v[p] = *reinterpret_cast<const f32x4*>(stg + r * PITCH + rc);
-        cx[p] = kLoads ? epi.prepare(m0 + wm0 + i * 32 + r, col, M, scol) : epi.blank(scol);
+      for (int p = 0; p < PASSES; ++p)
+        v[p] = *reinterpret_cast<const f32x4*>(stg + (p * ROWS_PER_PASS + rr) * PITCH + rc);
+      // the next block's row loads go out before this block's stores (or, for epilogues whose
+      // row context is too large to hold twice, this block's, waited for here)
+      Ctx cn[PASSES];
+      if constexpr (kLoads && kAhead) {
+        if (i + 1 < TM) prepare_block(i + 1, cn);
+      } else if constexpr (kLoads) {
+        prepare_block(i, cx);
+        FCV_WAIT_VMCNT0();
       }
-      if (kLoads) FCV_WAIT_VMCNT0();
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
       for (int p = 0; p < PASSES; ++p) {
         const int r = p * ROWS_PER_PASS + rr;
+        const Ctx x = kLoads ? cx[p] : epi.blank(scol);
         if constexpr (kFold)
-          epi.finish_biased(fold4(v[p], rstat[wm0 + i * 32 + r], sfold, scol.b), cx[p], scol,
+          epi.finish_biased(fold4(v[p], rstat[wm0 + i * 32 + r], sfold, scol.b), x, scol,
                             m0 + wm0 + i * 32 + r, col, M);
         else
-          epi.finish(v[p], cx[p], scol, m0 + wm0 + i * 32 + r, col, M);
+          epi.finish(v[p], x, scol, m0 + wm0 + i * 32 + r, col, M);
+      }
+      if constexpr (kLoads && kAhead) {
+        if (i + 1 < TM) {
+#pragma unroll
+          for (int p = 0; p < PASSES; ++p) cx[p] = cn[p];
+        }
       }
     }
   };
@@ -463,8 +507,11 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
 // ---- epilogues: v = C[row][col .. col+3] (col % 4 == 0) -------------------------------------
 // column(col): loads that depend on the column only (issued before the K loop);
 // row_loads(col0, n): whether columns [col0, col0 + n) need per-row data;
-// prepare(row, col, M, col_ctx): the row-dependent loads; blank(col_ctx): the context when there
-// are none; finish(v, ctx, col_ctx, row, col, M): the arithmetic and the stores.
+// kRowInfo / row_info(row): one int per row (a position, a document, a destination row), loaded
+// for the tile's rows before the K loop and kept in LDS;
+// prepare(row, col, M, col_ctx, info): the row-dependent loads (info = the row's row_info, or -1
+// past M); blank(col_ctx): the context when there are none; finish(v, ctx, col_ctx, row, col,
+// M): the arithmetic and the stores.
 
 __device__ __forceinline__ float4 add4(const f32x4& v, const float4& b) {
   return float4{v[0] + b.x, v[1] + b.y, v[2] + b.z, v[3] + b.w};
@@ -509,7 +556,8 @@ struct EpiBiasF32Bf16 {
   __device__ Ctx blank(const Col&) const { return {}; }
   __device__ bool direct(int) const { return false; }
   __device__ Col column(int col) const { return {ld4(bias + col)}; }
-  __device__ Ctx prepare(int, int, int, const Col&) const { return {}; }
+  static constexpr bool kRowInfo = false;
+  __device__ Ctx prepare(int, int, int, const Col&, int) const { return {}; }
   __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
     const bf16x4 yb = {f2bf(y.x), f2bf(y.y), f2bf(y.z), f2bf(y.w)};
@@ -533,7 +581,8 @@ struct EpiBiasF32 {
   __device__ Col column(int col) const {
     return {col < n_valid ? ld4(bias + col) : float4{0.f, 0.f, 0.f, 0.f}};
   }
-  __device__ Ctx prepare(int, int, int, const Col&) const { return {}; }
+  static constexpr bool kRowInfo = false;
+  __device__ Ctx prepare(int, int, int, const Col&, int) const { return {}; }
   __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
     if (row >= M || col >= n_valid) return;
@@ -556,8 +605,10 @@ struct EpiBiasF32RowMap {
   __device__ Col column(int col) const {
     return {col < n_valid ? ld4(bias + col) : float4{0.f, 0.f, 0.f, 0.f}};
   }
-  __device__ Ctx prepare(int row, int, int M, const Col&) const {
-    return {row < M ? row_map[row] : -1};
+  static constexpr bool kRowInfo = true;
+  __device__ int row_info(int row) const { return row_map[row]; }
+  __device__ Ctx prepare(int row, int, int M, const Col&, int info) const {
+    return {row < M ? info : -1};
   }
   __device__ void finish(const f32x4& v, const Ctx& x, const Col& c, int, int col, int) const {
     const float4 y = add4(v, c.b);
@@ -577,7 +628,8 @@ struct EpiBiasSiluBf16 {
   __device__ Ctx blank(const Col&) const { return {}; }
   __device__ bool direct(int) const { return false; }
   __device__ Col column(int col) const { return {ld4(bias + col)}; }
-  __device__ Ctx prepare(int, int, int, const Col&) const { return {}; }
+  static constexpr bool kRowInfo = false;
+  __device__ Ctx prepare(int, int, int, const Col&, int) const { return {}; }
   __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
     const bf16x4 yb = {f2bf(silu(y.x)), f2bf(silu(y.y)), f2bf(silu(y.z)), f2bf(silu(y.w))};
@@ -597,7 +649,8 @@ struct EpiBiasGeluBf16 {
   __device__ Ctx blank(const Col&) const { return {}; }
   __device__ bool direct(int) const { return false; }
   __device__ Col column(int col) const { return {ld4(bias + col)}; }
-  __device__ Ctx prepare(int, int, int, const Col&) const { return {}; }
+  static constexpr bool kRowInfo = false;
+  __device__ Ctx prepare(int, int, int, const Col&, int) const { return {}; }
   __device__ void finish(const f32x4& v, const Ctx& x, const Col& c, int row, int col, int M) const {
     finish_biased(add4(v, c.b), x, c, row, col, M);
   }
@@ -642,11 +695,15 @@ struct EpiGatedResidual {
     c.gn = kNext ? ld4(gnext + col) : float4{0.f, 0.f, 0.f, 0.f};
     return c;
   }
-  __device__ Ctx prepare(int row, int col, int M, const Col& c) const {
+  static constexpr bool kRowInfo = kPerDoc;  // the row's document
+  // a per-document gate row doubles the row context: one block of it at a time
+  static constexpr bool kPipelineRows = !kPerDoc;
+  __device__ int row_info(int row) const { return docid[row]; }
+  __device__ Ctx prepare(int row, int col, int M, const Col& c, int info) const {
     Ctx x;
     x.g = c.g;
     if constexpr (kPerDoc) {
-      if (row < M) x.g = ld4(gate + (long)docid[row] * mod_stride + col);
+      if (row < M) x.g = ld4(gate + (long)info * mod_stride + col);
     }
     x.x = buffer_ld4(buffer_over(h, (uint32_t)M * ldh * 4), (uint32_t)(row * ldh + col) * 4);
     return x;
@@ -694,14 +751,15 @@ struct EpiQkvRope {
   __device__ Ctx blank(const Col&) const { return {{1.0f, 1.0f}, {0.0f, 0.0f}}; }
   __device__ bool direct(int col) const { return col >= 2 * dim; }
   __device__ Col column(int col) const { return {ld4(bias + col)}; }
-  __device__ Ctx prepare(int row, int col, int M, const Col&) const {
+  // the row's position, clamped to the tables (pad rows run past the document)
+  static constexpr bool kRowInfo = true;
+  __device__ int row_info(int row) const { return min(pos[row], max_pos - 1); }
+  __device__ Ctx prepare(int row, int col, int M, const Col&, int info) const {
     Ctx c = {{1.0f, 1.0f}, {0.0f, 0.0f}};  // identity rotation where no angle is loaded
     const int cc = col % dim;
     if (col < 2 * dim && row < M && cc < rope_dim) {
-      // angles of the interleaved pairs (cc, cc+1), (cc+2, cc+3); pad rows run past the
-      // document, so the position is clamped
-      const int p = min(pos[row], max_pos - 1);
-      const long t = (long)p * (rope_dim >> 1) + (cc >> 1);
+      // angles of the interleaved pairs (cc, cc+1), (cc+2, cc+3)
+      const long t = (long)info * (rope_dim >> 1) + (cc >> 1);
       c.cs = *reinterpret_cast<const float2*>(rope_cos + t);
       c.sn = *reinterpret_cast<const float2*>(rope_sin + t);
     }
