@@ -48,19 +48,21 @@ __device__ __forceinline__ float half_sum(float v) {
 
 __global__ __launch_bounds__(256, 2) void attention_kernel(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ VT,
-    bf16* __restrict__ O, const int32_t* __restrict__ dstart, const int32_t* __restrict__ dlen,
-    const int32_t* __restrict__ tiles, int rp, int heads, int chunk, float scale_log2,
-    const int32_t* __restrict__ tiles_live) {
+    bf16* __restrict__ O, const int4* __restrict__ tiles, int rp, int heads, int chunk,
+    float scale_log2, const int32_t* __restrict__ tiles_live) {
   __shared__ __attribute__((aligned(16))) bf16 sK[2][TK][LDP];
   __shared__ __attribute__((aligned(16))) bf16 sV[2][HD][LDP];
 
   const int tile = blockIdx.x / heads;
   const int head = blockIdx.x % heads;
-  if (tiles_live && tile >= *tiles_live) return;  // past the live tiles of a capacity grid
-  const int doc = tiles[2 * tile];
-  const int q0 = tiles[2 * tile + 1];
-  const int doc_start = dstart[doc];
-  const int doc_end = doc_start + dlen[doc];
+  // the tile's entry and the live count are fetched together (an entry past the live count is
+  // inside the capacity-sized list and is not used)
+  const int4 td = tiles[tile];
+  const int live = tiles_live ? *tiles_live : 0x7fffffff;
+  if (tile >= live) return;  // past the live tiles of a capacity grid
+  const int doc_start = td.x;
+  const int doc_end = doc_start + td.y;
+  const int q0 = td.z;
   const int q_last = min(q0 + TQ - 1, doc_end - 1);
   int kv_end = doc_end;
   if (chunk > 0) {
@@ -254,15 +256,16 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
 }  // namespace
 
 hipError_t attention_varlen(const bf16* q, const bf16* k, const bf16* vt, bf16* o,
-                            const int32_t* doc_start, const int32_t* doc_len,
                             const int32_t* tiles, int n_tiles, int rp, int heads, int chunk,
                             hipStream_t stream, const int32_t* tiles_live) {
   if (n_tiles <= 0) return hipSuccess;
   // per-head K rows and V^T blocks are addressed by 32-bit buffer offsets
   if ((long)HD * rp * 2 >= (1L << 31)) return hipErrorInvalidValue;
   const float scale_log2 = 0.125f * 1.4426950408889634f;  // 64^-0.5 * log2(e)
+  if (reinterpret_cast<uintptr_t>(tiles) % 16 != 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(attention_kernel, dim3(n_tiles * heads), dim3(256), 0, stream, q, k, vt, o,
-                     doc_start, doc_len, tiles, rp, heads, chunk, scale_log2, tiles_live);
+                     reinterpret_cast<const int4*>(tiles), rp, heads, chunk, scale_log2,
+                     tiles_live);
   return hipGetLastError();
 }
 

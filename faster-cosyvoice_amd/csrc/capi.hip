@@ -88,7 +88,7 @@ Layout make_layout(const FcvDitDims& d, long rows, long n_docs) {
   L.cu_int = take((nd + 1) * 4);
   L.lens = take(nd * 4);
   L.cu_ext = take((nd + 1) * 4);
-  L.tiles = take(n_tiles * 2 * 4);
+  L.tiles = take(n_tiles * fcv::kAttnTileInts * 4);
   L.live = take(4 * 4);
   const long nt = std::max<long>(nd, kModGroup);  // time rows: per document, or a step group
   L.mod = take(nt * mod_width * 4);
@@ -291,8 +291,6 @@ int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, co
   int32_t* docid = m->at<int32_t>(m->L.docid);
   int32_t* pos = m->at<int32_t>(m->L.pos);
   int32_t* ext_row = m->at<int32_t>(m->L.ext_row);
-  int32_t* cu_int = m->at<int32_t>(m->L.cu_int);
-  int32_t* lens = m->at<int32_t>(m->L.lens);
   int32_t* tiles = m->at<int32_t>(m->L.tiles);
   float2* hstat = m->at<float2>(m->L.hstat);
   const bool folded = fold != nullptr && mod_stride == 0;
@@ -335,9 +333,9 @@ int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, co
     FCV_HIP(m->probe_end(FCV_STAGE_QKV, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_ATTENTION, l, s));
     for (int rep = m->launches(FCV_STAGE_ATTENTION, l); rep > 0; --rep)
-      FCV_HIP(fcv::attention_varlen(q, k, vt, obuf, cu_int, lens, tiles, m->tiles_cap, m->rp,
-                                    d.heads, m->mask_mode == FCV_MASK_CHUNK_CAUSAL ? m->chunk : 0,
-                                    s, live_tiles));
+      FCV_HIP(fcv::attention_varlen(q, k, vt, obuf, tiles, m->tiles_cap, m->rp, d.heads,
+                                    m->mask_mode == FCV_MASK_CHUNK_CAUSAL ? m->chunk : 0, s,
+                                    live_tiles));
     FCV_HIP(m->probe_end(FCV_STAGE_ATTENTION, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_OUT_PROJ, l, s));
     FCV_HIP(fcv::gemm_gated_residual(obuf, D, B(w.out_w) + (long)l * D * D, D,
@@ -464,7 +462,8 @@ int fcv_dit_plan_capacity(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int
   }
   const int rows_int = cu_int[n_docs];
 
-  // attention tiles: (doc, first internal query row), most expensive first (LPT order)
+  // attention tiles: {doc start, doc length, first query row, 0} in internal rows, most
+  // expensive first (LPT order)
   struct T { int doc, q0; long cost; };
   std::vector<T> tl;
   for (int d = 0; d < n_docs; ++d) {
@@ -479,10 +478,12 @@ int fcv_dit_plan_capacity(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int
   }
   std::stable_sort(tl.begin(), tl.end(), [](const T& a, const T& b) { return a.cost > b.cost; });
   std::vector<int32_t> tiles_host;
-  tiles_host.reserve(tl.size() * 2);
+  tiles_host.reserve(tl.size() * fcv::kAttnTileInts);
   for (const T& t : tl) {
-    tiles_host.push_back(t.doc);
+    tiles_host.push_back(cu_int[t.doc]);
+    tiles_host.push_back(lens[t.doc]);
     tiles_host.push_back(t.q0);
+    tiles_host.push_back(0);
   }
 
   const Layout L = make_layout(m->dims, rows_cap, docs_cap);

@@ -95,15 +95,15 @@ hipError_t gemv_bias_silu_bf16(const bf16* a, int lda, const bf16* W, int ldw, c
                                int M, int N, int K, bf16* out, int ldo, hipStream_t stream);
 
 // ---- attention ----------------------------------------------------------------------------
-// Varlen attention, head_dim 64.  Document d starts at row doc_start[d] (a multiple of 8)
-// and has doc_len[d] real rows; tiles[i] = {doc, first query row}.  q, k: [heads][rp][64],
-// vt: [heads][64][rp].  chunk == 0: full attention inside each document; chunk > 0: key
-// visible iff (key_pos / chunk) <= (query_pos / chunk).  n_tiles is the grid's capacity;
-// tiles_live (when not null) holds the live tile count.
+// Varlen attention, head_dim 64.  tiles (16-byte aligned) holds one 4-int entry per tile of
+// kAttnTileQ queries: {document start row (a multiple of 8), document length, first query
+// row, unused}.  q, k: [heads][rp][64], vt: [heads][64][rp].  chunk == 0: full attention
+// inside each document; chunk > 0: key visible iff (key_pos / chunk) <= (query_pos / chunk).
+// n_tiles is the grid's capacity; tiles_live (when not null) holds the live tile count.
 hipError_t attention_varlen(const bf16* q, const bf16* k, const bf16* vt, bf16* o,
-                            const int32_t* doc_start, const int32_t* doc_len,
                             const int32_t* tiles, int n_tiles, int rp, int heads, int chunk,
                             hipStream_t stream, const int32_t* tiles_live = nullptr);
+constexpr int kAttnTileInts = 4;  // ints per tile entry
 constexpr int kAttnTileQ = 128;
 
 // ---- causal grouped conv position embedding (64 channels per group) -------------------------
