@@ -49,13 +49,13 @@ __device__ __forceinline__ float hw_exp2(float x) { return __builtin_amdgcn_exp2
 __device__ __forceinline__ float hw_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
 // tanh-approximated GELU (torch nn.GELU(approximate="tanh")):
-//   0.5 x (1 + tanh(u)) = x / (1 + e^(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3).
+//   0.5 x (1 + tanh(u)) = x / (1 + e^(-2u)),  u = sqrt(2/pi) (x + 0.044715 x^3),
+// with -2 u log2(e) = x (c0 + c1 x^2): three VALU operations before the exponential.
 // For x -> -inf, e^(-2u) overflows to inf and the result is -0; for x -> +inf it is x.
 __device__ __forceinline__ float gelu_tanh(float x) {
-  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-  const float k1 = 0.044715f;
-  const float u = k0 * fmaf(k1 * x, x * x, x);
-  return x * hw_rcp(1.0f + hw_exp2(-2.8853900817779268f * u));  // -2 log2(e) u
+  const float c0 = -2.302208198144325f;    // -2 log2(e) sqrt(2/pi)
+  const float c1 = -0.1029432395800235f;   // c0 * 0.044715
+  return x * hw_rcp(1.0f + hw_exp2(x * fmaf(c1, x * x, c0)));
 }
 
 // Mish: x * tanh(softplus(x)).  With e = e^x, tanh(log(1 + e)) = n / (n + 2), n = e (e + 2).
