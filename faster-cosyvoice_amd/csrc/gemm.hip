@@ -9,9 +9,10 @@
 // per CU);
 // each wave a sub-tile of 32x32 MFMA tiles.  Operands go straight from global memory into LDS
 // with global_load_lds_dwordx4 (no register staging, no ds_write; scalar base and LDS address,
-// per-lane 32-bit offset) through a ring of slices (by default two stages of K = 64: one
-// wave-level copy fills 1 KB of LDS = 8 rows x 128 B, so every L2 request is a full 128-byte
-// line).  The 16-byte chunks of a row sit at a row-rotated position, so 16 consecutive rows
+// per-lane 32-bit offset) through a ring of slices (two stages of K = 64, three for the small
+// 32x128 tile, whose few workgroups per CU leave the copy latency exposed: FF2 at ~1k rows
+// 19.6 -> 17.3 us; one wave-level copy fills 1 KB of LDS = 8 rows x 128 B, so every L2 request
+// is a full 128-byte line).  The 16-byte chunks of a row sit at a row-rotated position, so 16 consecutive rows
 // read at one chunk index hit 16 distinct 16-byte bank groups.  Inside a slice the fragments of
 // k-step ks+1 are read while the MFMAs of k-step ks run, and the loop is rotated so that a
 // slice's last k-step runs after the barrier that publishes the next slice.  The tile shape is
@@ -804,7 +805,7 @@ using Tile160x256 = TileCfg<160, 256, 1, 4>;
 using Tile128x256 = TileCfg<128, 256, 2, 4>;
 using Tile256x128 = TileCfg<256, 128, 4, 2>;
 using Tile128x128 = TileCfg<128, 128, 2, 2>;
-using Tile32x128 = TileCfg<32, 128, 1, 4>;
+using Tile32x128 = TileCfg<32, 128, 1, 4, 64, 3>;
 using Tile96x128 = TileCfg<96, 128, 1, 4>;
 
 template <class C, class Epi>
