@@ -834,9 +834,12 @@ hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, in
 // workgroups per CU, which its rate includes; 160x256 runs one wave per SIMD, so it rates low
 // although it fills more CUs; 32x128 is rated low so it only wins when the larger shapes leave
 // most CUs idle, as for the 128-column output projection.  96x128 (four 96x32 waves, two
-// workgroups per CU) is only offered for the 1024-column GEMMs (out-projection, FF2), where it
-// was measured fastest from ~2k to ~6k rows (a request group's share of a batch): its rate puts
-// it between 32x128 below and 192x256 above.  The choice only changes which rows
+// workgroups per CU) sits between 32x128 below and 192x256 above: it wins for the 1024-column
+// GEMMs from ~2k to ~6k rows (a request group's share of a batch) and for FF1 and QKV at one to
+// three thousand rows (a single request or a short stream); a sweep of the four block GEMMs
+// over 1.1k-9.3k rows with every shape forced found the estimate's pick within 1 % of the
+// fastest shape, except QKV at 1.1k rows (128x128, 6 % slower than 96x128) and at 6.2k rows
+// (4 %).  The choice only changes which rows
 // and columns share a workgroup: every output element still accumulates its K slices in the
 // same order, so results are bitwise identical for every tile shape (batch invariance holds).
 constexpr int kCus = 256;
@@ -850,7 +853,7 @@ inline int choose_tile(int M, int N) {
   float best_t = 3.0e38f;
   for (int c = 0; c < kTileShapes; ++c) {
     const int bm = kTileShape[c][0], bn = kTileShape[c][1];
-    if (N % bn != 0 || (c == 7 && N != 1024)) continue;
+    if (N % bn != 0) continue;
     const long tiles = (long)((M + bm - 1) / bm) * (N / bn);
     const long per_cu = (tiles + kCus - 1) / kCus;
     const float t = (float)per_cu * bm * bn / kTileRate[c];
