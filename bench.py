@@ -419,8 +419,8 @@ def main() -> int:
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: this build runs the estimator on a single MI355X "
-              "(documents shard across GPUs without any collective; see DESIGN.md)",
+        print("bench.py measures one GPU: the estimator runs on a single MI355X "
+              "(documents would shard across GPUs without any collective)",
               file=sys.stderr)
         return 2
     if not 1 <= args.steps <= 64:

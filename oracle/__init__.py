@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product imports this package: only
 ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` use it, and only as the checker (or as the timed CPU baseline),
+``bench.py`` use it, and only as the reference they compare against (or as the timed CPU baseline),
 never as the thing measured or shipped.
 
 ``dit_oracle`` restates the reference's fp32 torch DiT (padded SDPA with

@@ -16,7 +16,7 @@ from __future__ import annotations
 
 import torch
 
-VEL_TOL = 1e-2  # per-step velocity rel-L2 against the fp32 oracle
+VEL_TOL = 1e-2  # per-step velocity rel-L2 against the fp32 oracle (the parity bar)
 
 # 22 blocks; the CFG pair of one 550-frame request (prompt 250), t = 0.5
 SHARP22 = dict(depth=22, seed=41, qk_std=0.05, gate_bias=0.2)

@@ -1,7 +1,7 @@
 """GPU parity of the HIP estimator against the fp32 CPU oracle and the reference golden vectors.
 
-Tolerances: per-step velocity rel-L2 <= 1e-2 vs the fp32 path,
-mel rel-L2 <= 2e-2 after 10 Euler steps.  Where the oracle is given the same bf16-rounded
+Tolerances: per-step velocity rel-L2 <= 1e-2 vs the fp32 path, mel rel-L2 <= 2e-2 after 10
+Euler steps.  Where the oracle is given the same bf16-rounded
 weights the GPU uses, the remaining error is activation rounding only and the bound is tighter.
 """
 
