@@ -70,11 +70,49 @@ __device__ __forceinline__ void conv_store1(const HiftConv& p, long row, int c, 
   static_cast<T*>(p.out)[i] = v;
 }
 
+__device__ __forceinline__ float4 ld4f(const float* q) { return *reinterpret_cast<const float4*>(q); }
+
+// conv_store1 for the four consecutive fp32 channels c .. c + 3 of one row, with 16-byte loads
+// and stores (same operations in the same order, so the results are bit-identical)
+__device__ __forceinline__ void conv_store4(const HiftConv& p, long row, int c, const f32x4& acc) {
+  const float4 b = ld4f(static_cast<const float*>(p.bias) + c);
+  float v[4] = {acc[0] + b.x, acc[1] + b.y, acc[2] + b.z, acc[3] + b.w};
+  const long i = row * p.ldo + c;
+  if (p.add) {
+    const float4 a = ld4f(static_cast<const float*>(p.add) + row * p.ld_add + c);
+    v[0] = v[0] + a.x; v[1] = v[1] + a.y; v[2] = v[2] + a.z; v[3] = v[3] + a.w;
+  }
+  if (p.mode != HIFT_ACC_WRITE) {
+    const float4 a = ld4f(static_cast<const float*>(p.accin) + i);
+    v[0] = a.x + v[0]; v[1] = a.y + v[1]; v[2] = a.z + v[2]; v[3] = a.w + v[3];
+    if (p.mode == HIFT_ACC_ADD_DIV)
+      for (int e = 0; e < 4; ++e) v[e] = v[e] / p.div;
+  }
+  // the Snakes one channel at a time: four inlined sinf at once spill
+  if (p.snake_out) {
+#pragma unroll 1
+    for (int e = 0; e < 4; ++e) v[e] = snake(v[e], p.alpha[c + e], p.inv_alpha[c + e]);
+  }
+  if (p.out2) {
+    float w[4];
+#pragma unroll 1
+    for (int e = 0; e < 4; ++e) w[e] = snake(v[e], p.alpha2[c + e], p.inv_alpha2[c + e]);
+    *reinterpret_cast<float4*>(static_cast<float*>(p.out2) + i) = float4{w[0], w[1], w[2], w[3]};
+  }
+  *reinterpret_cast<float4*>(static_cast<float*>(p.out) + i) = float4{v[0], v[1], v[2], v[3]};
+}
+
 // The 16x16x4 accumulators of lane (li, lg) hold, for the tile's channel base cb:
 //   fp32: channels cb + 4 lg + e;  fp64: channels cb + 4 e + lg  (e = 0..3)
 template <typename T>
 __device__ void conv_store(const HiftConv& p, long row, int cb, int lg,
                            const typename Vec4<T>::type& acc) {
+  if constexpr (sizeof(T) == 4) {
+    if (p.vec4 && cb + 4 * lg + 3 < p.cout) {
+      conv_store4(p, row, cb + 4 * lg, acc);
+      return;
+    }
+  }
   for (int e = 0; e < 4; ++e) {
     const int c = sizeof(T) == 4 ? cb + 4 * lg + e : cb + 4 * e + lg;
     if (c < p.cout) conv_store1<T>(p, row, c, acc[e]);
@@ -421,10 +459,19 @@ __global__ __launch_bounds__(256) void copy_live_kernel(const float* __restrict_
 
 unsigned blocks_for(long n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
+bool aligned16(const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; }
+
 template <typename T>
-hipError_t launch_conv(const HiftConv& p, const HiftDocs* docs, hipStream_t stream) {
-  if (p.rows_out <= 0) return hipSuccess;
-  if (p.cin_pad % 16 != 0) return hipErrorInvalidValue;
+hipError_t launch_conv(const HiftConv& p_in, const HiftDocs* docs, hipStream_t stream) {
+  if (p_in.rows_out <= 0) return hipSuccess;
+  if (p_in.cin_pad % 16 != 0) return hipErrorInvalidValue;
+  HiftConv p = p_in;
+  // 16-byte epilogue accesses when every row pitch and base the epilogue touches allows them
+  p.vec4 = sizeof(T) == 4 && p.ldo % 4 == 0 && aligned16(p.out) && aligned16(p.bias) &&
+           (!p.add || (p.ld_add % 4 == 0 && aligned16(p.add))) &&
+           (p.mode == HIFT_ACC_WRITE || aligned16(p.accin)) &&
+           (!p.snake_out || (aligned16(p.alpha) && aligned16(p.inv_alpha))) &&
+           (!p.out2 || (aligned16(p.out2) && aligned16(p.alpha2) && aligned16(p.inv_alpha2)));
   const dim3 grid((p.rows_out + kTileR - 1) / kTileR, (p.cout + kTileC - 1) / kTileC);
   if (p.cin_pad % 32 == 0)
     hipLaunchKernelGGL((hift_conv_kernel<T, 32>), grid, dim3(256), 0, stream, p, docs);

@@ -45,6 +45,7 @@ struct HiftConv {
   int snake_out;
   void* out; int ldo;
   void* out2; const float* alpha2; const float* inv_alpha2;  // out2 = snake(y) (optional)
+  int vec4;                                // set by the launch: 16-byte epilogue accesses
 };
 
 hipError_t hift_conv_f32(const HiftConv& p, const HiftDocs* docs, hipStream_t stream);
