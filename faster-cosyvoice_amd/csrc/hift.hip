@@ -43,9 +43,11 @@ __device__ __forceinline__ int doc_of(const int32_t* cu, int n_docs, int row) {
   return lo;
 }
 
-// Snake(x) = x + sin(a x)^2 / (a + 1e-9), with inv = 1 / (a + 1e-9) precomputed in fp32
+// Snake(x) = x + sin(a x)^2 / (a + 1e-9), with inv = 1 / (a + 1e-9) precomputed in fp32.
+// sin by v_sin_f32 on the fractional part of the argument in turns (v_fract_f32 is exact).
 __device__ __forceinline__ float snake(float x, float a, float inv) {
-  const float s = sinf(x * a);
+  const float turns = (x * a) * 0.15915494309189535f;
+  const float s = __builtin_amdgcn_sinf(__builtin_amdgcn_fractf(turns));
   return x + inv * (s * s);
 }
 
