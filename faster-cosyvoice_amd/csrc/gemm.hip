@@ -35,6 +35,7 @@
 // to give each XCD a contiguous range of tiles; inside that range tiles are visited in groups of
 // GROUP_M M-tiles x all N-tiles (M fastest), keeping the group's A rows and W columns inside
 // one XCD's 4 MB L2.
+#include <cstdlib>
 #include <type_traits>
 
 #include "kernels.hpp"
@@ -862,6 +863,16 @@ inline int choose_tile(int M, int N) {
   return best;
 }
 
+// FCV_GEMM_TILE=<shape index> forces one tile shape wherever it divides N: a test hook, since
+// every shape must give the same bits (the tile choice never changes an element's K order).
+inline int forced_tile(int N) {
+  const char* e = std::getenv("FCV_GEMM_TILE");
+  if (e == nullptr || *e == '\0') return -1;
+  const int c = std::atoi(e);
+  if (c < 0 || c >= kTileShapes || N % kTileShape[c][1] != 0) return -1;
+  return c;
+}
+
 // M: the rows the grid covers (a capacity when m_live holds the live count, which must not
 // exceed it).  The tile shape is chosen from M; it never changes an element's K summation
 // order, so a layout's results are the same under any capacity.
@@ -875,7 +886,8 @@ hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, 
   if (N % 128 != 0 || K % 64 != 0 || lda % 8 != 0 || ldw % 8 != 0) return hipErrorInvalidValue;
   // the copies address A and W by 32-bit byte offsets from their bases
   if ((long)M * lda * 2 >= (1L << 32) || (long)N * ldw * 2 >= (1L << 32)) return hipErrorInvalidValue;
-  switch (choose_tile(M, N)) {
+  const int forced = forced_tile(N);
+  switch (forced >= 0 ? forced : choose_tile(M, N)) {
     case 0: return launch_tile<Tile256x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     case 2: return launch_tile<Tile128x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);

@@ -431,6 +431,26 @@ def test_batch_invariance_and_determinism(fcv, stress2):
             off += n
 
 
+def test_every_gemm_tile_shape_gives_the_same_bits(fcv, stress2, monkeypatch):
+    """The GEMM tile shape only decides which rows and columns share a workgroup, never an
+    element's K order.  Forcing each of the eight shapes (FCV_GEMM_TILE, wherever it divides
+    the output width) reproduces the default choice bit for bit, with the full and the
+    chunk-causal mask and with one shared t (the folded LayerNorm) and one t per document."""
+    sd, est = stress2
+    lengths = [90, 300, 17, 150]
+    x, mu, cond, spks, t_doc = random_packed(lengths, seed=8)
+    for streaming in (False, True):
+        for t in (torch.tensor([0.42]), t_doc):
+            monkeypatch.delenv("FCV_GEMM_TILE", raising=False)
+            ref = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming)
+            for shape in range(8):
+                say(f"[tiles] streaming={streaming} n_t={t.numel()} shape {shape}")
+                monkeypatch.setenv("FCV_GEMM_TILE", str(shape))
+                got = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming)
+                assert torch.equal(got, ref), (streaming, t.numel(), shape)
+    monkeypatch.delenv("FCV_GEMM_TILE", raising=False)
+
+
 def test_streaming_prefix_stability_gate_a(fcv, stress2):
     """Reference Gate A (tests/gpu/test_flashinfer_streaming_estimator.py:58-89): with the
     chunk-causal mask the first floor(160/50)*50 frames of T=160 and T=200 agree; with full
