@@ -19,6 +19,7 @@ namespace {
 
 constexpr int kTileR = 64;  // time rows per workgroup
 constexpr int kTileC = 64;  // output channels per workgroup
+constexpr long kSmallTileBelow = 256;  // 64x64 tiles per launch under which 32x32 tiles run
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
@@ -121,16 +122,24 @@ __device__ void conv_store(const HiftConv& p, long row, int cb, int lg,
   }
 }
 
-// BK input channels of one tap per chunk (cin_pad % BK == 0); each loader thread moves BK / 16
-// groups of 4 elements per operand, each lane feeds k = 16 m + 4 lg + s at MFMA step (m, s)
-template <typename T, int BK>
+// BK input channels of one tap per chunk (cin_pad % BK == 0), each lane feeding
+// k = 16 m + 4 lg + s at MFMA step (m, s).  A workgroup owns TS time rows x TS output channels
+// (TS = 64, or 32 for launches too small to give every CU a 64x64 tile); its four waves each
+// own a TS/2 x TS/2 quarter.  Loaders: at TS = 64 every thread moves BK / 16 groups of 4
+// elements of one weight row and one input row; at TS = 32 waves 0-1 move the weight rows and
+// waves 2-3 the input rows, the same groups each.  Every output element accumulates the chunks
+// in the same order with the same lane/slot -> k rule at both sizes, so the tile size does not
+// change a result.
+template <typename T, int BK, int TS>
 __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p,
                                                         const HiftDocs* __restrict__ docs) {
   using VT = typename Vec4<T>::type;
   constexpr int PITCH = BK + 4;  // LDS row pitch in elements (conflict-free 16-byte reads)
   constexpr int G = BK / 16;
-  __shared__ __attribute__((aligned(16))) T sA[2][kTileC][PITCH];
-  __shared__ __attribute__((aligned(16))) T sB[2][kTileR][PITCH];
+  constexpr int NQ = TS / 32;    // 16x16 accumulator tiles per wave along each side
+  static_assert(TS == 64 || TS == 32, "tile size");
+  __shared__ __attribute__((aligned(16))) T sA[2][TS][PITCH];
+  __shared__ __attribute__((aligned(16))) T sB[2][TS][PITCH];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -139,17 +148,19 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p,
   const int li = lane & 15, lg = lane >> 4;
   const int n_docs = docs->n;
   const int rows_out = docs->b[n_docs];  // live rows (the grid covers the capacity)
-  const int r0 = blockIdx.x * kTileR;
+  const int r0 = blockIdx.x * TS;
   if (r0 >= rows_out) return;
-  const int co0 = blockIdx.y * kTileC;
+  const int co0 = blockIdx.y * TS;
   const int cpt = p.cin_pad / BK;
   const int KC = p.k * cpt;
   const long kcin = (long)p.k * p.cin_pad;
 
-  // loader roles: weight row lr / input row lr, 4-element quarter lq of the 16-channel chunk
-  const int lr = tid >> 2, lq = tid & 3;
+  // loader roles: weight row / input row lr, 4-element quarter lq of each 16-channel group;
+  // at TS = 32 a thread loads the weights (ld_w) or the inputs (ld_x), not both
+  const int lr = TS == 64 ? tid >> 2 : (tid & 127) >> 2, lq = tid & 3;
+  const bool ld_w = TS == 64 || tid < 128, ld_x = TS == 64 || tid >= 128;
   const int r = r0 + lr;
-  const bool valid = r < rows_out;
+  const bool valid = ld_x && r < rows_out;
   int in_base = 0, in_len = 0, pos = 0;
   if (valid) {
     const int d = doc_of(docs->b, n_docs, r);
@@ -173,7 +184,7 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p,
     const T* xr = X + (long)(in_base + q) * p.ldx + c0;
 #pragma unroll
     for (int m = 0; m < G; ++m) {
-      a[m] = *reinterpret_cast<const VT*>(W + (long)kc * BK + 16 * m);
+      if (ld_w) a[m] = *reinterpret_cast<const VT*>(W + (long)kc * BK + 16 * m);
       b[m] = VT{T(0), T(0), T(0), T(0)};
       if (live) b[m] = *reinterpret_cast<const VT*>(xr + 16 * m);
     }
@@ -189,33 +200,33 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p,
           for (int e = 0; e < 4; ++e) bm[e] = bm[e] > 0.0f ? bm[e] : bm[e] * p.slope;
         }
       }
-      *reinterpret_cast<VT*>(&sA[buf][lr][16 * m + 4 * lq]) = a[m];
-      *reinterpret_cast<VT*>(&sB[buf][lr][16 * m + 4 * lq]) = bm;
+      if (ld_w) *reinterpret_cast<VT*>(&sA[buf][lr][16 * m + 4 * lq]) = a[m];
+      if (ld_x) *reinterpret_cast<VT*>(&sB[buf][lr][16 * m + 4 * lq]) = bm;
     }
   };
 
-  VT acc[2][2];
+  VT acc[NQ][NQ];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < NQ; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b) acc[a][b] = VT{T(0), T(0), T(0), T(0)};
+    for (int b = 0; b < NQ; ++b) acc[a][b] = VT{T(0), T(0), T(0), T(0)};
 
   auto compute = [&](int cur) {
 #pragma unroll
     for (int m = 0; m < G; ++m) {
-      VT av[2], bv[2];
+      VT av[NQ], bv[NQ];
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
-        av[a] = *reinterpret_cast<const VT*>(&sA[cur][wc * 32 + a * 16 + li][16 * m + 4 * lg]);
+      for (int a = 0; a < NQ; ++a)
+        av[a] = *reinterpret_cast<const VT*>(&sA[cur][wc * (TS / 2) + a * 16 + li][16 * m + 4 * lg]);
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
-        bv[b] = *reinterpret_cast<const VT*>(&sB[cur][wt * 32 + b * 16 + li][16 * m + 4 * lg]);
+      for (int b = 0; b < NQ; ++b)
+        bv[b] = *reinterpret_cast<const VT*>(&sB[cur][wt * (TS / 2) + b * 16 + li][16 * m + 4 * lg]);
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int a = 0; a < NQ; ++a)
 #pragma unroll
-          for (int b = 0; b < 2; ++b) acc[a][b] = mfma_16x16x4(av[a][s], bv[b][s], acc[a][b]);
+          for (int b = 0; b < NQ; ++b) acc[a][b] = mfma_16x16x4(av[a][s], bv[b][s], acc[a][b]);
     }
   };
 
@@ -245,15 +256,15 @@ __global__ __launch_bounds__(256) void hift_conv_kernel(const HiftConv p,
 
   // D[i = channel][j = row]: lane holds row li and four channels of each 16x16 tile
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    const int rr = r0 + wt * 32 + b * 16 + li;
+  for (int b = 0; b < NQ; ++b) {
+    const int rr = r0 + wt * (TS / 2) + b * 16 + li;
     if (rr >= rows_out) continue;
     const int d = doc_of(docs->b, n_docs, rr);
     const int pp = rr - docs->b[d];
     const long row_w = p.reflect ? (long)docs->b[d] + d + 1 + pp : rr;
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const int cb = co0 + wc * 32 + a * 16;
+    for (int a = 0; a < NQ; ++a) {
+      const int cb = co0 + wc * (TS / 2) + a * 16;
       conv_store<T>(p, row_w, cb, lg, acc[a][b]);
       // reflection padding (1, 0): row 0 of the document repeats the result's row 1
       if (p.reflect && pp == 1) conv_store<T>(p, (long)docs->b[d] + d, cb, lg, acc[a][b]);
@@ -474,11 +485,22 @@ hipError_t launch_conv(const HiftConv& p_in, const HiftDocs* docs, hipStream_t s
            (p.mode == HIFT_ACC_WRITE || aligned16(p.accin)) &&
            (!p.snake_out || (aligned16(p.alpha) && aligned16(p.inv_alpha))) &&
            (!p.out2 || (aligned16(p.out2) && aligned16(p.alpha2) && aligned16(p.inv_alpha2)));
+  // 64x64 tiles, or 32x32 where 64x64 tiles would not give every CU one (the grid covers the
+  // capacity, so a captured call and its replays use the same size; results do not depend on it)
+  const long tiles64 = (long)((p.rows_out + kTileR - 1) / kTileR) * ((p.cout + kTileC - 1) / kTileC);
+  if (tiles64 < kSmallTileBelow) {
+    const dim3 grid((p.rows_out + 31) / 32, (p.cout + 31) / 32);
+    if (p.cin_pad % 32 == 0)
+      hipLaunchKernelGGL((hift_conv_kernel<T, 32, 32>), grid, dim3(256), 0, stream, p, docs);
+    else
+      hipLaunchKernelGGL((hift_conv_kernel<T, 16, 32>), grid, dim3(256), 0, stream, p, docs);
+    return hipGetLastError();
+  }
   const dim3 grid((p.rows_out + kTileR - 1) / kTileR, (p.cout + kTileC - 1) / kTileC);
   if (p.cin_pad % 32 == 0)
-    hipLaunchKernelGGL((hift_conv_kernel<T, 32>), grid, dim3(256), 0, stream, p, docs);
+    hipLaunchKernelGGL((hift_conv_kernel<T, 32, 64>), grid, dim3(256), 0, stream, p, docs);
   else
-    hipLaunchKernelGGL((hift_conv_kernel<T, 16>), grid, dim3(256), 0, stream, p, docs);
+    hipLaunchKernelGGL((hift_conv_kernel<T, 16, 64>), grid, dim3(256), 0, stream, p, docs);
   return hipGetLastError();
 }
 
