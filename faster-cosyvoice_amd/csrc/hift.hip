@@ -7,7 +7,7 @@
 // time step (consecutive in fp32; four apart in fp64, whose 16x16 result is laid out by rows
 // 4 e + lane / 16).  Operands go through LDS K-contiguous, 32 (or 16) input channels of one tap
 // per chunk, with a register-prefetched double buffer.  A workgroup owns 64 time rows x 64
-// output channels.  Activations that sit between two convolutions are fused: LeakyReLU into the
+// output channels (32 x 32 in launches too small to give every CU a 64 x 64 tile).  Activations that sit between two convolutions are fused: LeakyReLU into the
 // input prologue, bias, ELU, residual add, Snake and the resblock mean into the epilogue, and
 // the epilogue can also write Snake(y) as a second output for the next conv.
 #include <math.h>
