@@ -12,6 +12,8 @@
 // the epilogue can also write Snake(y) as a second output for the next conv.
 #include <math.h>
 
+#include <cstdlib>
+
 #include "hift.hpp"
 
 namespace fcv {
@@ -486,9 +488,12 @@ hipError_t launch_conv(const HiftConv& p_in, const HiftDocs* docs, hipStream_t s
            (!p.snake_out || (aligned16(p.alpha) && aligned16(p.inv_alpha))) &&
            (!p.out2 || (aligned16(p.out2) && aligned16(p.alpha2) && aligned16(p.inv_alpha2)));
   // 64x64 tiles, or 32x32 where 64x64 tiles would not give every CU one (the grid covers the
-  // capacity, so a captured call and its replays use the same size; results do not depend on it)
+  // capacity, so a captured call and its replays use the same size; results do not depend on it).
+  // FCV_HIFT_TILE=32 or 64 forces one size: a test hook, since both must give the same bits.
   const long tiles64 = (long)((p.rows_out + kTileR - 1) / kTileR) * ((p.cout + kTileC - 1) / kTileC);
-  if (tiles64 < kSmallTileBelow) {
+  const char* forced = std::getenv("FCV_HIFT_TILE");
+  const int force = forced ? std::atoi(forced) : 0;
+  if (force == 32 || (force != 64 && tiles64 < kSmallTileBelow)) {
     const dim3 grid((p.rows_out + 31) / 32, (p.cout + 31) / 32);
     if (p.cin_pad % 32 == 0)
       hipLaunchKernelGGL((hift_conv_kernel<T, 32, 32>), grid, dim3(256), 0, stream, p, docs);

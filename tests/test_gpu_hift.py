@@ -94,6 +94,25 @@ def test_packed_requests_equal_requests_alone(hift):
         assert torch.equal(p, alone)
 
 
+def test_tile_size_does_not_change_the_waveform(hift, monkeypatch):
+    """The conv kernel's 64x64 and 32x32 tiles (the second for launches too small to fill the
+    CUs) sum every output in the same order: forcing either size (FCV_HIFT_TILE) reproduces
+    the default call bit for bit, for a short streaming chunk and a packed pair (the fixture's
+    noise table holds 64 frames of source per request)."""
+    dims, sd, buf, v = hift
+    g = torch.Generator().manual_seed(23)
+    for frames, fin in (([60], [False]), ([40, 55], [True, False])):
+        mels = [torch.randn(80, n, generator=g).to("cuda:0") for n in frames]
+        monkeypatch.delenv("FCV_HIFT_TILE", raising=False)
+        ref = v.inference_batched(mels, fin, graph=False)
+        for size in ("32", "64"):
+            say(f"[hift tiles] {frames} forced {size}")
+            monkeypatch.setenv("FCV_HIFT_TILE", size)
+            got = v.inference_batched(mels, fin, graph=False)
+            assert all(torch.equal(a, b) for a, b in zip(got, ref)), (frames, size)
+    monkeypatch.delenv("FCV_HIFT_TILE", raising=False)
+
+
 def test_short_non_final_chunk_is_rejected(hift):
     _, _, _, v = hift
     with pytest.raises(ValueError):
