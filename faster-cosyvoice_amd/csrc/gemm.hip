@@ -808,6 +808,7 @@ using Tile256x128 = TileCfg<256, 128, 4, 2>;
 using Tile128x128 = TileCfg<128, 128, 2, 2>;
 using Tile32x128 = TileCfg<32, 128, 1, 4, 64, 3>;
 using Tile96x128 = TileCfg<96, 128, 1, 4>;
+using Tile96x128x3 = TileCfg<96, 128, 1, 4, 64, 3>;  // one workgroup per CU
 
 template <class C, class Epi>
 hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
@@ -894,7 +895,12 @@ hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, 
     case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     case 5: return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
-    case 7: return launch_tile<Tile96x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+    case 7:
+      // where the tiles fit one round of CUs, a third ring stage gives each copy more lead (the
+      // tile then holds a CU alone); with more tiles the two-stage form's two per CU win
+      if ((long)((M + 95) / 96) * (N / 128) <= kCus)
+        return launch_tile<Tile96x128x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+      return launch_tile<Tile96x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     default: return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
   }
 }
