@@ -809,6 +809,7 @@ using Tile128x128 = TileCfg<128, 128, 2, 2>;
 using Tile32x128 = TileCfg<32, 128, 1, 4, 64, 3>;
 using Tile96x128 = TileCfg<96, 128, 1, 4>;
 using Tile96x128x3 = TileCfg<96, 128, 1, 4, 64, 3>;  // one workgroup per CU
+using Tile128x128x3 = TileCfg<128, 128, 2, 2, 64, 3>;  // one workgroup per CU
 
 template <class C, class Epi>
 hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
@@ -901,7 +902,10 @@ hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, 
       if ((long)((M + 95) / 96) * (N / 128) <= kCus)
         return launch_tile<Tile96x128x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
       return launch_tile<Tile96x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
-    default: return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+    default:
+      if ((long)((M + 127) / 128) * (N / 128) <= kCus)
+        return launch_tile<Tile128x128x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+      return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
   }
 }
 
