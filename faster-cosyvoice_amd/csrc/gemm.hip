@@ -810,6 +810,7 @@ using Tile32x128 = TileCfg<32, 128, 1, 4, 64, 3>;
 using Tile96x128 = TileCfg<96, 128, 1, 4>;
 using Tile96x128x3 = TileCfg<96, 128, 1, 4, 64, 3>;  // one workgroup per CU
 using Tile128x128x3 = TileCfg<128, 128, 2, 2, 64, 3>;  // one workgroup per CU
+using Tile32x128x4 = TileCfg<32, 128, 1, 4, 64, 4>;
 
 template <class C, class Epi>
 hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
@@ -894,7 +895,10 @@ hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, 
     case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     case 2: return launch_tile<Tile128x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
-    case 5: return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+    case 5:
+      if ((long)((M + 31) / 32) * (N / 128) <= kCus)
+        return launch_tile<Tile32x128x4>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+      return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
     case 7:
       // where the tiles fit one round of CUs, a third ring stage gives each copy more lead (the
