@@ -60,13 +60,12 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
 
   const bf16* wg = w + (long)g * taps * CG * CG;
   const int lw_r = tid >> 3;  // 0..31
-  bf16x8 rw[2];
-  auto fetch = [&](int j) {
+  auto fetch = [&](bf16x8 (&rw)[2], int j) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       rw[i] = *reinterpret_cast<const bf16x8*>(wg + ((long)j * CG + lw_r + 32 * i) * CG + chunk_c);
   };
-  auto stash = [&](int buf) {
+  auto stash = [&](const bf16x8 (&rw)[2], int buf) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       *reinterpret_cast<bf16x8*>(&sW[buf][lw_r + 32 * i][chunk_c]) = rw[i];
@@ -85,18 +84,8 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[t][e] = 0.0f;
 
-  fetch(0);
-  stash(0);
-  __syncthreads();
   const bf16x8 zero8 = {};
-  for (int j = 0; j < taps; ++j) {
-    const int cur = j & 1;
-    // the next tap's weights are fetched and stashed unconditionally (the last tap re-reads
-    // its own slice into the idle buffer), so no path leaves the fetch pending and the compiler
-    // does not wait for it before this tap's MFMAs; the fence keeps the loads at the top of the
-    // tap (left alone, the scheduler sinks them next to the stash and waits on them there)
-    fetch(min(j + 1, taps - 1));
-    __builtin_amdgcn_sched_barrier(0);
+  auto tap = [&](int j, int buf) {
     // rows before the row's document start read as zero (per-document causal padding)
     const bool live = lpos + j >= halo;
 #pragma unroll
@@ -105,12 +94,33 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
       const bf16x8 xb = live ? v : zero8;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const bf16x8 wa = *reinterpret_cast<const bf16x8*>(&sW[cur][t * 32 + fr][ks * 16 + fh * 8]);
+        const bf16x8 wa = *reinterpret_cast<const bf16x8*>(&sW[buf][t * 32 + fr][ks * 16 + fh * 8]);
         acc[t] = mfma32(wa, xb, acc[t]);
       }
     }
-    stash(cur ^ 1);
+  };
+  // Weights run two taps ahead of the MFMAs: tap j+1's slice (loaded during tap j-1) is stashed
+  // while tap j+2's loads are in flight, so a stash never waits on loads issued in its own tap
+  // (a workgroup alone on its CU would otherwise wait out a load round trip every tap).  Taps
+  // past the last re-read the last slice, so every path issues the same loads.
+  bf16x8 ra[2], rb[2];
+  fetch(ra, 0);
+  stash(ra, 0);
+  fetch(ra, min(1, taps - 1));
+  __syncthreads();
+  for (int j = 0; j < taps; j += 2) {
+    fetch(rb, min(j + 2, taps - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    tap(j, 0);
+    stash(ra, 1);
     __syncthreads();
+    if (j + 1 < taps) {
+      fetch(ra, min(j + 3, taps - 1));
+      __builtin_amdgcn_sched_barrier(0);
+      tap(j + 1, 1);
+      stash(rb, 0);
+      __syncthreads();
+    }
   }
 
   // epilogue (the loop's last barrier freed the window and weight buffers)
