@@ -13,8 +13,9 @@
 // 32x128 tile, whose few workgroups per CU leave the copy latency exposed: FF2 at ~1k rows
 // 19.6 -> 17.3 us; and where a launch's tiles fit one round of CUs, so each holds a CU alone,
 // three for 96x128 and 128x128 and four for 32x128; one wave-level copy fills 1 KB of LDS =
-// 8 rows x 128 B, so every L2 request is a full 128-byte line).  The 16-byte chunks of a row sit at a row-rotated position, so 16 consecutive rows
-// read at one chunk index hit 16 distinct 16-byte bank groups.  Inside a slice the fragments of
+// 8 rows x 128 B, so every L2 request is a full 128-byte line).  The 16-byte chunks of a row
+// sit at a row-rotated position, so 16 consecutive rows read at one chunk index hit 16 distinct
+// 16-byte bank groups.  Inside a slice the fragments of
 // k-step ks+1 are read while the MFMAs of k-step ks run, and the loop is rotated so that a
 // slice's last k-step runs after the barrier that publishes the next slice.  The tile shape is
 // chosen per call from the tile rounds over the 256 CUs and per-shape rates.
