@@ -83,21 +83,34 @@ def _solver_buffers(runner: _PackedRunner, dims, rows_cap: int,
     return bufs
 
 
-def _schedule_buffer(estimator: DiTEstimator, n_steps: int) -> torch.Tensor:
-    """The estimator's persistent buffer for an ``n_steps`` solve schedule (the modulation rows
-    every request group reads, ``fcv_dit_schedule``).  One per step count, kept for the
-    estimator's life: its pointer is part of the graphs captured over it."""
-    bufs = estimator.__dict__.setdefault("_schedule_bufs", {})
-    buf = bufs.get(n_steps)
-    if buf is None:
-        nbytes = _lib.load().fcv_dit_schedule_bytes(estimator._require(), n_steps)
-        if nbytes == 0:
-            raise ValueError("n_steps must be in [1, 64]")
-        buf = torch.empty(nbytes, dtype=torch.uint8, device=estimator.device)
-        if buf.data_ptr() % 256:
-            raise RuntimeError("schedule buffer is not 256-byte aligned")
-        bufs[n_steps] = buf
-    return buf
+def _schedule(estimator: DiTEstimator, n_steps: int, t_arr,
+              stream: torch.cuda.Stream) -> tuple[torch.Tensor, torch.cuda.Event]:
+    """The estimator's ``n_steps`` solve schedule: every step's modulation rows
+    (``fcv_dit_schedule``), which every request group's solve reads.  They depend
+    only on the weights, which are fixed once finalized, and on the cosine schedule's t values,
+    which ``n_steps`` fixes, so they are computed once per step count, on ``stream``, and kept
+    for the estimator's life (the buffer's pointer is part of the graphs captured over it).
+    Returns the buffer and an event recorded after its computation, which a solve on another
+    stream waits for."""
+    cache = estimator.__dict__.setdefault("_schedules", {})
+    hit = cache.get(n_steps)
+    if hit is not None:
+        return hit
+    lib = _lib.load()
+    nbytes = lib.fcv_dit_schedule_bytes(estimator._require(), n_steps)
+    if nbytes == 0:
+        raise ValueError("n_steps must be in [1, 64]")
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=estimator.device)
+    if buf.data_ptr() % 256:
+        raise RuntimeError("schedule buffer is not 256-byte aligned")
+    with torch.cuda.stream(stream):
+        buf.record_stream(stream)
+        _lib.check(lib.fcv_dit_schedule(estimator._require(), t_arr, n_steps, buf.data_ptr(),
+                                        buf.numel(), stream.cuda_stream))
+        done = torch.cuda.Event()
+        done.record(stream)
+    cache[n_steps] = (buf, done)
+    return buf, done
 
 
 def _stream_for(runner: _PackedRunner) -> torch.cuda.Stream:
@@ -129,10 +142,9 @@ def _solve_on(runner: _PackedRunner, dims, noise: torch.Tensor, mu: torch.Tensor
               cond: torch.Tensor, spks: torch.Tensor, lengths: list[int], t_arr, dt_arr,
               n_steps: int, cfg_rate: float, streaming: bool, use_graph: bool,
               stream: torch.cuda.Stream, bucketed: bool,
-              schedule: torch.Tensor | None = None) -> torch.Tensor:
-    """One packed CFG solve on ``runner``, enqueued on ``stream`` (the caller orders it).  With
-    ``schedule`` (filled by ``fcv_dit_schedule``) the solve reads its modulation rows there
-    instead of computing them."""
+              schedule: torch.Tensor) -> torch.Tensor:
+    """One packed CFG solve on ``runner``, enqueued on ``stream`` (the caller orders it).  It
+    reads its modulation rows from ``schedule`` (filled by ``fcv_dit_schedule``)."""
     rc, b = sum(lengths), len(lengths)
     capacity = capacity_bucket(2 * rc, 2 * b) if bucketed else None
     with torch.cuda.stream(stream):
@@ -148,18 +160,11 @@ def _solve_on(runner: _PackedRunner, dims, noise: torch.Tensor, mu: torch.Tensor
         buf["cond"][rc:2 * rc].zero_()
         buf["spks"][:b].copy_(spks)
         buf["spks"][b:2 * b].zero_()
-        lib = _lib.load()
-        if schedule is None:
-            _lib.check(lib.fcv_dit_solve(
-                runner._require(), buf["x"].data_ptr(), buf["mu"].data_ptr(),
-                buf["cond"].data_ptr(), buf["spks"].data_ptr(), t_arr, dt_arr, n_steps,
-                float(cfg_rate), int(bool(use_graph)), stream.cuda_stream))
-        else:
-            _lib.check(lib.fcv_dit_solve_scheduled(
-                runner._require(), buf["x"].data_ptr(), buf["mu"].data_ptr(),
-                buf["cond"].data_ptr(), buf["spks"].data_ptr(), dt_arr, n_steps,
-                float(cfg_rate), schedule.data_ptr(), schedule.numel(), int(bool(use_graph)),
-                stream.cuda_stream))
+        _lib.check(_lib.load().fcv_dit_solve_scheduled(
+            runner._require(), buf["x"].data_ptr(), buf["mu"].data_ptr(),
+            buf["cond"].data_ptr(), buf["spks"].data_ptr(), dt_arr, n_steps,
+            float(cfg_rate), schedule.data_ptr(), schedule.numel(), int(bool(use_graph)),
+            stream.cuda_stream))
         return buf["x"][:rc].clone()
 
 
@@ -179,8 +184,10 @@ def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.T
     second half) on its own handle over the shared weights and its own stream, all launched
     before any is waited for.  One group's tail rounds and bandwidth-bound phases then overlap
     the other's matrix work.  The modulation rows of the schedule (one pass over the AdaLN
-    weights) are computed once, on the caller's stream, and every group reads them.  A document's result does not depend on what it is packed with,
-    so the rows are bit-identical to one packed batch of all requests.
+    weights) are computed on the caller's stream by the first
+    solve of a step count and kept (``_schedule``); every group of every later solve reads
+    them.  A document's result does not depend on what it is packed with, so the rows are
+    bit-identical to one packed batch of all requests.
 
     ``bucketed`` plans each group into its capacity bucket (``capacity_bucket``), so a new
     layout in a bucket that has been captured replays its graph; False plans the exact layout.
@@ -203,11 +210,14 @@ def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.T
     dt_arr = (_lib.c_float * n_steps)(*dts)
     current = torch.cuda.current_stream(dev)
     runners = estimator.lanes(len(groups))
+    schedule, scheduled = _schedule(estimator, n_steps, t_arr, current)
     if len(groups) == 1:
         stream = _stream_for(estimator)
         stream.wait_stream(current)
+        stream.wait_event(scheduled)
         result = _solve_on(estimator, estimator.dims, noise, mu, cond, spks, lengths, t_arr,
-                           dt_arr, n_steps, cfg_rate, streaming, use_graph, stream, bucketed)
+                           dt_arr, n_steps, cfg_rate, streaming, use_graph, stream, bucketed,
+                           schedule)
         current.wait_stream(stream)
         return result
     offs = [0]
@@ -218,12 +228,9 @@ def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.T
                   for g in groups]
     parts = []
     streams = [_stream_for(r) for r in runners]
-    schedule = _schedule_buffer(estimator, n_steps)
-    _lib.check(_lib.load().fcv_dit_schedule(estimator._require(), t_arr, n_steps,
-                                            schedule.data_ptr(), schedule.numel(),
-                                            current.cuda_stream))
     for s in streams:  # every group waits for the caller's work only, not for each other
         s.wait_stream(current)
+        s.wait_event(scheduled)
     for runner, stream, g, rows in zip(runners, streams, groups, group_rows):
         with torch.cuda.stream(stream):
             out = _solve_on(runner, estimator.dims, noise[rows], mu[rows], cond[rows], spks[g],
