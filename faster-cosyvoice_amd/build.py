@@ -45,8 +45,19 @@ def library_path() -> Path:
     return PKG_DIR / LIB_NAME
 
 
+# The DiT sources compile without floating-point contraction: every fused multiply-add there is
+# an explicit fmaf.  With contraction allowed the compiler fuses a product and its fp16
+# conversion into v_fma_mix (one rounding instead of two) in some template instantiations and
+# not in others, so an element's fp16 bits would depend on the GEMM tile shape, and with it on
+# the batch a document is packed with.
+EXACT_SOURCES = {"gemm.hip", "gemv.hip", "attention.hip", "conv.hip", "elementwise.hip", "capi.hip"}
+EXACT_FLAGS = ["-ffp-contract=off"]
+
+
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    extra = EXACT_FLAGS if src.name in EXACT_SOURCES else []
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o",
+           str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")

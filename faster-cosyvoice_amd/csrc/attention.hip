@@ -1,4 +1,4 @@
-// Varlen flash attention over cu_seqlens for head_dim 64 on gfx950 (MFMA 32x32x16 bf16).
+// Varlen flash attention over cu_seqlens for head_dim 64 on gfx950 (MFMA 32x32x16 f16).
 //
 // One workgroup = one tile of 128 queries of one document x one head; 4 waves x 32 queries.
 // The kernel computes S^T = K Q^T so that the fp32 accumulator of S^T (lane l owns query
@@ -23,7 +23,7 @@ namespace {
 constexpr int TQ = kAttnTileQ;  // queries per workgroup
 constexpr int TK = 64;          // keys per LDS tile
 constexpr int HD = 64;          // head dim
-constexpr int LDP = 72;         // padded LDS row (bf16 elements)
+constexpr int LDP = 72;         // padded LDS row (f16 elements)
 
 // v_exp_f32 without the library's denormal range reduction: results below 2^-126 flush to 0,
 // which only drops probabilities that are negligible next to the row maximum's 1.
@@ -47,11 +47,11 @@ __device__ __forceinline__ float half_sum(float v) {
 }
 
 __global__ __launch_bounds__(256, 2) void attention_kernel(
-    const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ VT,
-    bf16* __restrict__ O, const int4* __restrict__ tiles, int rp, int heads, int chunk,
+    const f16* __restrict__ Q, const f16* __restrict__ K, const f16* __restrict__ VT,
+    f16* __restrict__ O, const int4* __restrict__ tiles, int rp, int heads, int chunk,
     float scale_log2, const int32_t* __restrict__ tiles_live) {
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][TK][LDP];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][HD][LDP];
+  __shared__ __attribute__((aligned(16))) f16 sK[2][TK][LDP];
+  __shared__ __attribute__((aligned(16))) f16 sV[2][HD][LDP];
 
   const int tile = blockIdx.x / heads;
   const int head = blockIdx.x % heads;
@@ -82,17 +82,17 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
   const int key_lim =
       chunk > 0 ? min(kv_end, doc_start + (max(q_pos, 0) / chunk + 1) * chunk) : kv_end;
 
-  const bf16* Qh = Q + (long)head * rp * HD;
-  const bf16* Kh = K + (long)head * rp * HD;
-  const bf16* Vh = VT + (long)head * HD * rp;
+  const f16* Qh = Q + (long)head * rp * HD;
+  const f16* Kh = K + (long)head * rp * HD;
+  const f16* Vh = VT + (long)head * HD * rp;
 
   // Q^T fragments (B operand): query ql, dims 16*ks + 8*hl + 0..7
-  bf16x8 qf[4];
+  f16x8 qf[4];
   {
     const int qr = min(q_row, doc_end - 1);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      qf[ks] = *reinterpret_cast<const bf16x8*>(Qh + (long)qr * HD + ks * 16 + hl * 8);
+      qf[ks] = *reinterpret_cast<const f16x8*>(Qh + (long)qr * HD + ks * 16 + hl * 8);
   }
 
   // tile loaders: each thread moves 2 x 16 bytes of K and 2 x 16 bytes of V^T, through raw
@@ -105,11 +105,11 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
   const int lr = tid >> 3;         // 0..31
   const int lc = (tid & 7) * 8;    // 0..56
   const __amdgpu_buffer_rsrc_t k_rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(Kh), (short)0, rp * HD * 2, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(Kh), (short)0, rp * HD * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t v_rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(Vh), (short)0, HD * rp * 2, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(Vh), (short)0, HD * rp * 2, 0x00020000);
   const uint32_t k_lane = (uint32_t)(lr * HD + lc) * 2, v_lane = (uint32_t)(lr * rp) * 2;
-  bf16x8 rk[2], rv[2];
+  f16x8 rk[2], rv[2];
   int vcnt = 8;  // keys of this thread's V^T chunks below kv_end
   auto fetch = [&](int kb) {
     const int k0 = kb + lc;
@@ -117,10 +117,10 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       rk[i] = __builtin_bit_cast(
-          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(
                       k_rsrc, k_lane + (uint32_t)(kb + 32 * i) * HD * 2, 0, 0));
       rv[i] = __builtin_bit_cast(
-          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+          f16x8, __builtin_amdgcn_raw_buffer_load_b128(
                       v_rsrc, v_lane + (uint32_t)(32 * i * rp + k0) * 2, 0, 0));
     }
   };
@@ -129,12 +129,12 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) rv[i][e] = e < vcnt ? rv[i][e] : f2bf(0.0f);
+        for (int e = 0; e < 8; ++e) rv[i][e] = e < vcnt ? rv[i][e] : (f16)0.0f;
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      *reinterpret_cast<bf16x8*>(&sK[buf][lr + 32 * i][lc]) = rk[i];
-      *reinterpret_cast<bf16x8*>(&sV[buf][lr + 32 * i][lc]) = rv[i];
+      *reinterpret_cast<f16x8*>(&sK[buf][lr + 32 * i][lc]) = rk[i];
+      *reinterpret_cast<f16x8*>(&sV[buf][lr + 32 * i][lc]) = rv[i];
     }
   };
 
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
       for (int e = 0; e < 16; ++e) s[kt][e] = 0.0f;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[cur][kt * 32 + ql][ks * 16 + hl * 8]);
+        f16x8 kf = *reinterpret_cast<const f16x8*>(&sK[cur][kt * 32 + ql][ks * 16 + hl * 8]);
         s[kt] = mfma32(kf, qf[ks], s[kt]);
       }
     }
@@ -205,14 +205,16 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
       m_run = m_new;
     }
     float psum = 0.0f;
-    bf16x8 pf[4];
+    f16x8 pf[4];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const float p = fast_exp2(fmaf(s[kt][e], scale_log2, -m_new));
         psum += p;
-        pf[kt * 2 + (e >> 3)][e & 7] = f2bf(p);
+        // a plain cast: p is an exponential, not a product, so no multiply can be fused into
+        // the conversion here
+        pf[kt * 2 + (e >> 3)][e & 7] = (f16)p;
       }
     }
     l_run += psum;
@@ -224,10 +226,10 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
       const int kbase = (st >> 1) * 32 + (st & 1) * 16 + hl * 4;
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
-        const bf16* vrow = &sV[cur][dt * 32 + ql][0];
-        bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow + kbase);
-        bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + kbase + 8);
-        bf16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        const f16* vrow = &sV[cur][dt * 32 + ql][0];
+        f16x4 lo = *reinterpret_cast<const f16x4*>(vrow + kbase);
+        f16x4 hi = *reinterpret_cast<const f16x4*>(vrow + kbase + 8);
+        f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         acc_o[dt] = mfma32(vf, pf[st], acc_o[dt]);
       }
     }
@@ -239,15 +241,15 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
   const float l_tot = half_sum(l_run);
   const float inv = 1.0f / l_tot;
   if (q_row < doc_end) {
-    bf16* dst = O + (long)q_row * heads * HD + head * HD;
+    f16* dst = O + (long)q_row * heads * HD + head * HD;
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         const int d = dt * 32 + a * 8 + hl * 4;
-        bf16x4 pk = {f2bf(acc_o[dt][4 * a + 0] * inv), f2bf(acc_o[dt][4 * a + 1] * inv),
-                     f2bf(acc_o[dt][4 * a + 2] * inv), f2bf(acc_o[dt][4 * a + 3] * inv)};
-        *reinterpret_cast<bf16x4*>(dst + d) = pk;
+        f16x4 pk = f2h4(acc_o[dt][4 * a + 0] * inv, acc_o[dt][4 * a + 1] * inv,
+                        acc_o[dt][4 * a + 2] * inv, acc_o[dt][4 * a + 3] * inv);
+        *reinterpret_cast<f16x4*>(dst + d) = pk;
       }
     }
   }
@@ -255,7 +257,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(
 
 }  // namespace
 
-hipError_t attention_varlen(const bf16* q, const bf16* k, const bf16* vt, bf16* o,
+hipError_t attention_varlen(const f16* q, const f16* k, const f16* vt, f16* o,
                             const int32_t* tiles, int n_tiles, int rp, int heads, int chunk,
                             hipStream_t stream, const int32_t* tiles_live) {
   if (n_tiles <= 0) return hipSuccess;

@@ -10,7 +10,7 @@
 #include "kernels.hpp"
 #include "status.hpp"
 
-using fcv::bf16;
+using fcv::f16;
 
 namespace {
 
@@ -43,7 +43,7 @@ struct Layout {
   // byte offsets inside the workspace
   size_t h, nbuf, obuf, q, k, vt, u, ain, vbuf;
   size_t docid, pos, ext_row, docid_ext, pos_ext, cu_int, lens, cu_ext, tiles, live;
-  size_t mod, tsin, t1, t2, tbuf, fold, hstat;
+  size_t mod, tsin, t1, t2, tbuf;
   size_t total;
 };
 
@@ -53,9 +53,6 @@ long internal_rows_bound(long rows, long n_docs) { return rows + 7 * n_docs; }
 long tiles_bound(long rows, long n_docs) {
   return internal_rows_bound(rows, n_docs) / fcv::kAttnTileQ + n_docs + 1;
 }
-
-// floats of adaln_fold's output per modulation row
-long fold_width(const FcvDitDims& d) { return (long)d.depth * (6L * d.dim + 2L * d.ff_dim); }
 
 // Workspace of a capacity: at most `rows` caller rows in at most `n_docs` documents.
 Layout make_layout(const FcvDitDims& d, long rows, long n_docs) {
@@ -96,9 +93,6 @@ Layout make_layout(const FcvDitDims& d, long rows, long n_docs) {
   L.t1 = take(nt * (long)d.dim * 2);
   L.t2 = take(nt * (long)d.dim * 2);
   L.tbuf = take(kMaxSteps * 4);
-  // LayerNorm fold: column terms per step of a group (adaln_fold), row statistics per row
-  L.fold = take((long)kModGroup * fold_width(d) * 4);
-  L.hstat = take(rp * (long)fcv::kStatChunks * 8);
   L.total = off;
   return L;
 }
@@ -159,12 +153,11 @@ struct FcvDit {
     probe_repeat = 1;
   }
 
-  // The probed launch of a stage: in block 1, the first whose LayerNorms fold into its GEMMs
-  // and so the launch every later block repeats (block 0 for a one-block model, and for the
-  // LN-modulate pass, which the fold leaves in block 0 only); layer -1 = outside the blocks.
+  // The probed launch of a stage: in block 1 (block 0 for a one-block model); layer -1 =
+  // outside the blocks.
   bool probed(int stage, int layer) const {
     if (stage != probe_stage || probe_count >= probe_pairs) return false;
-    const int target = (stage == FCV_STAGE_LN_MOD || dims.depth == 1) ? 0 : 1;
+    const int target = dims.depth == 1 ? 0 : 1;
     return layer < 0 || layer == target;
   }
   hipError_t probe_begin(int stage, int layer, hipStream_t s) {
@@ -184,38 +177,33 @@ namespace {
 // timestep embedding -> SiLU(temb) -> every block's AdaLN modulation in one projection, for
 // n_t time values (device t): row i of `mod` (mod_width floats) belongs to t[i]
 // (TimestepEmbedding modules.py:606-616; _project_modulations flashinfer_dit.py:430-445).
-// With `fold` (n_t <= kModGroup), also the LayerNorm fold's column terms of each row (row i at
-// fold + i * fold_width).  tsin / t1 / t2: scratch for n_t rows of 256 / dim / dim bf16.
-int modulation_rows(FcvDit* m, const float* t, int n_t, bf16* tsin, bf16* t1, bf16* t2,
-                    float* mod, float* fold, hipStream_t s) {
+// tsin / t1 / t2: scratch for n_t rows of 256 / dim / dim fp16.
+int modulation_rows(FcvDit* m, const float* t, int n_t, f16* tsin, f16* t1, f16* t2,
+                    float* mod, hipStream_t s) {
   const FcvDitWeights& w = m->w;
   const int D = m->dims.dim;
-  auto B = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
+  auto B = [](const void* p) { return reinterpret_cast<const f16*>(p); };
   FCV_HIP(fcv::timestep_sinusoid(t, n_t, 256, tsin, s));
-  FCV_HIP(fcv::gemm_bias_silu_bf16(tsin, 256, B(w.temb_w1), 256, w.temb_b1, n_t, D, 256, t1, D, s));
-  FCV_HIP(fcv::gemm_bias_silu_bf16(t1, D, B(w.temb_w2), D, w.temb_b2, n_t, D, D, t2, D, s));
+  FCV_HIP(fcv::gemm_bias_silu_f16(tsin, 256, B(w.temb_w1), 256, w.temb_b1, n_t, D, 256, t1, D, s));
+  FCV_HIP(fcv::gemm_bias_silu_f16(t1, D, B(w.temb_w2), D, w.temb_b2, n_t, D, D, t2, D, s));
   FCV_HIP(m->probe_begin(FCV_STAGE_ADALN, -1, s));
   for (int rep = m->launches(FCV_STAGE_ADALN, -1); rep > 0; --rep)
     FCV_HIP(fcv::gemm_bias_f32(t2, D, B(w.ada_w), D, w.ada_b, n_t, (int)m->mod_width, D, mod,
                                (int)m->mod_width, (int)m->mod_width, s));
-  if (fold)
-    FCV_HIP(fcv::adaln_fold(B(w.qkv_w), w.qkv_b, B(w.ff1_w), w.ff1_b, m->dims.depth, D,
-                            m->dims.ff_dim, mod, m->mod_width, n_t, fold, s));
   FCV_HIP(m->probe_end(FCV_STAGE_ADALN, -1, s));
   return FCV_OK;
 }
 
-// modulation_rows into the workspace's mod (and fold) region
-int compute_modulations(FcvDit* m, const float* t, int n_t, bool fold, hipStream_t s) {
-  return modulation_rows(m, t, n_t, m->at<bf16>(m->L.tsin), m->at<bf16>(m->L.t1),
-                         m->at<bf16>(m->L.t2), m->at<float>(m->L.mod),
-                         fold ? m->at<float>(m->L.fold) : nullptr, s);
+// modulation_rows into the workspace's mod region
+int compute_modulations(FcvDit* m, const float* t, int n_t, hipStream_t s) {
+  return modulation_rows(m, t, n_t, m->at<f16>(m->L.tsin), m->at<f16>(m->L.t1),
+                         m->at<f16>(m->L.t2), m->at<float>(m->L.mod), s);
 }
 
 // A solve schedule (fcv_dit_schedule): device t values, scratch for one group of kModGroup
-// time rows, then every step's modulation row and fold terms.
+// time rows, then every step's modulation row.
 struct Schedule {
-  size_t t, tsin, t1, t2, mod, fold, total;
+  size_t t, tsin, t1, t2, mod, total;
 };
 Schedule schedule_layout(const FcvDitDims& d, long n_steps) {
   Schedule S{};
@@ -231,76 +219,63 @@ Schedule schedule_layout(const FcvDitDims& d, long n_steps) {
   S.t1 = take((long)kModGroup * d.dim * 2);
   S.t2 = take((long)kModGroup * d.dim * 2);
   S.mod = take(n_steps * mod_width * 4);
-  S.fold = take(n_steps * fold_width(d) * 4);
   S.total = off;
   return S;
 }
 
 int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
-               const float* mod, long mod_stride, const float* fold, float* v_out, hipStream_t s);
+               const float* mod, long mod_stride, float* v_out, hipStream_t s);
 
 // one estimator evaluation: modulations for t (1 shared value or one per document), then the
-// network; `mod_row`, when not null, is an already computed shared-t modulation row and
-// `fold_row` its LayerNorm fold terms
+// network; `mod_row`, when not null, is an already computed shared-t modulation row
 int run_forward(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
-                const float* t, int n_t, const float* mod_row, const float* fold_row,
-                float* v_out, hipStream_t s) {
+                const float* t, int n_t, const float* mod_row, float* v_out, hipStream_t s) {
   FCV_HIP(m->probe_begin(FCV_STAGE_FORWARD, -1, s));
   const float* mod = mod_row;
-  const float* fold = fold_row;
   long mod_stride = 0;
   if (!mod) {
-    // one t for every document: the LayerNorms fold into the GEMMs; one t per document: they
-    // run as LN-modulate passes
-    int rc = compute_modulations(m, t, n_t, n_t == 1, s);
+    int rc = compute_modulations(m, t, n_t, s);
     if (rc != FCV_OK) return rc;
     mod = m->at<float>(m->L.mod);
     mod_stride = (n_t == 1) ? 0 : m->mod_width;
-    fold = (n_t == 1) ? m->at<float>(m->L.fold) : nullptr;
   }
-  int rc = run_blocks(m, x, mu, cond, spks, mod, mod_stride, fold, v_out, s);
+  int rc = run_blocks(m, x, mu, cond, spks, mod, mod_stride, v_out, s);
   if (rc != FCV_OK) return rc;
   FCV_HIP(m->probe_end(FCV_STAGE_FORWARD, -1, s));
   return FCV_OK;
 }
 
-// `fold` (mod_stride 0 only): adaln_fold's terms for the modulation row.  Then the LayerNorm
-// before every GEMM but the first block's QKV and proj_out runs inside the GEMMs: each gated
-// residual writes bf16(h * g) of the next LayerNorm and h's row statistics, and the next QKV or
-// FF1 GEMM applies the normalization in its epilogue.  Without it, each LayerNorm + modulation
-// is a pass of its own (ln_mod_kernel) that writes the GEMM's normalized bf16 input.
+// The network on packed rows.  Every LayerNorm + modulation before a GEMM is a pass of its own
+// (ln_mod_kernel, fp32 statistics) that writes the GEMM's normalized fp16 input: the same
+// tensor the reference materializes (flashinfer_kernels.py:84-145).
 int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, const float* spks,
-               const float* mod, long mod_stride, const float* fold, float* v_out,
-               hipStream_t s) {
+               const float* mod, long mod_stride, float* v_out, hipStream_t s) {
   const FcvDitDims& d = m->dims;
   const FcvDitWeights& w = m->w;
   // grids cover the plan's capacity; the kernels read the live counts
   const int R = m->rint_cap, D = d.dim, F = d.ff_dim, mel = d.mel_dim;
   const int32_t* live_rows = m->live() + fcv::kLiveRows;
   const int32_t* live_tiles = m->live() + fcv::kLiveTiles;
-  auto B = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
+  auto B = [](const void* p) { return reinterpret_cast<const f16*>(p); };
 
   float* h = m->at<float>(m->L.h);
-  bf16* nbuf = m->at<bf16>(m->L.nbuf);
-  bf16* obuf = m->at<bf16>(m->L.obuf);
-  bf16* q = m->at<bf16>(m->L.q);
-  bf16* k = m->at<bf16>(m->L.k);
-  bf16* vt = m->at<bf16>(m->L.vt);
-  bf16* u = m->at<bf16>(m->L.u);
-  bf16* ain = m->at<bf16>(m->L.ain);
+  f16* nbuf = m->at<f16>(m->L.nbuf);
+  f16* obuf = m->at<f16>(m->L.obuf);
+  f16* q = m->at<f16>(m->L.q);
+  f16* k = m->at<f16>(m->L.k);
+  f16* vt = m->at<f16>(m->L.vt);
+  f16* u = m->at<f16>(m->L.u);
+  f16* ain = m->at<f16>(m->L.ain);
   int32_t* docid = m->at<int32_t>(m->L.docid);
   int32_t* pos = m->at<int32_t>(m->L.pos);
   int32_t* ext_row = m->at<int32_t>(m->L.ext_row);
   int32_t* tiles = m->at<int32_t>(m->L.tiles);
-  float2* hstat = m->at<float2>(m->L.hstat);
-  const bool folded = fold != nullptr && mod_stride == 0;
-  const long fw = 6L * D + 2L * F;  // fold terms per block: u_qkv, v_qkv, u_ff1, v_ff1
 
   // input projection + causal conv position embedding (InputEmbedding dit.py:84-98)
   FCV_HIP(fcv::pack_inputs(x, cond, mu, spks, docid, ext_row, R, mel, ain, s, live_rows));
   FCV_HIP(m->probe_begin(FCV_STAGE_IN_PROJ, -1, s));
   for (int rep = m->launches(FCV_STAGE_IN_PROJ, -1); rep > 0; --rep)
-    FCV_HIP(fcv::gemm_bias_f32_bf16(ain, 4 * mel, B(w.in_w), 4 * mel, w.in_b, R, D, 4 * mel, h,
+    FCV_HIP(fcv::gemm_bias_f32_f16(ain, 4 * mel, B(w.in_w), 4 * mel, w.in_b, R, D, 4 * mel, h,
                                     nbuf, D, s, live_rows));
   FCV_HIP(m->probe_end(FCV_STAGE_IN_PROJ, -1, s));
   FCV_HIP(m->probe_begin(FCV_STAGE_CONV, -1, s));
@@ -314,22 +289,17 @@ int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, co
   // transformer blocks (DiTBlock.forward modules.py:516-530)
   for (int l = 0; l < d.depth; ++l) {
     const long base = (long)l * 6 * D;
-    const float* fl = folded ? fold + l * fw : nullptr;
-    const bool fold_qkv = folded && l > 0;  // block 0's input comes from the conv, not a GEMM
-    if (!fold_qkv) {
-      FCV_HIP(m->probe_begin(FCV_STAGE_LN_MOD, l, s));
-      for (int rep = m->launches(FCV_STAGE_LN_MOD, l); rep > 0; --rep)
-        FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 0),
-                                         (int)(base + D), docid, nbuf, s, live_rows));
-      FCV_HIP(m->probe_end(FCV_STAGE_LN_MOD, l, s));
-    }
+    FCV_HIP(m->probe_begin(FCV_STAGE_LN_MOD, l, s));
+    for (int rep = m->launches(FCV_STAGE_LN_MOD, l); rep > 0; --rep)
+      FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 0), (int)(base + D),
+                                       docid, nbuf, s, live_rows));
+    FCV_HIP(m->probe_end(FCV_STAGE_LN_MOD, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_QKV, l, s));
     for (int rep = m->launches(FCV_STAGE_QKV, l); rep > 0; --rep)
       FCV_HIP(fcv::gemm_qkv_rope(nbuf, D, B(w.qkv_w) + (long)l * 3 * D * D, D,
-                                 fold_qkv ? fl + 3 * D : w.qkv_b + (long)l * 3 * D, R, D, d.heads,
-                                 pos, w.rope_cos, w.rope_sin, d.rope_dim, d.max_pos, q, k, vt,
-                                 m->rp, s, live_rows, fold_qkv ? fl : nullptr,
-                                 fold_qkv ? hstat : nullptr));
+                                 w.qkv_b + (long)l * 3 * D, R, D, d.heads, pos, w.rope_cos,
+                                 w.rope_sin, d.rope_dim, d.max_pos, q, k, vt, m->rp, s,
+                                 live_rows));
     FCV_HIP(m->probe_end(FCV_STAGE_QKV, l, s));
     FCV_HIP(m->probe_begin(FCV_STAGE_ATTENTION, l, s));
     for (int rep = m->launches(FCV_STAGE_ATTENTION, l); rep > 0; --rep)
@@ -340,26 +310,19 @@ int run_blocks(FcvDit* m, const float* x, const float* mu, const float* cond, co
     FCV_HIP(m->probe_begin(FCV_STAGE_OUT_PROJ, l, s));
     FCV_HIP(fcv::gemm_gated_residual(obuf, D, B(w.out_w) + (long)l * D * D, D,
                                      w.out_b + (long)l * D, R, D, D, h, D, mod + base + 2 * D,
-                                     mod_stride, docid, s, live_rows,
-                                     folded ? mod + base + 4 * D : nullptr, nbuf, hstat));
+                                     mod_stride, docid, s, live_rows));
     FCV_HIP(m->probe_end(FCV_STAGE_OUT_PROJ, l, s));
-    if (!folded)
-      FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 3 * D),
-                                       (int)(base + 4 * D), docid, nbuf, s, live_rows));
+    FCV_HIP(fcv::layer_norm_modulate(h, D, R, mod, mod_stride, (int)(base + 3 * D),
+                                     (int)(base + 4 * D), docid, nbuf, s, live_rows));
     FCV_HIP(m->probe_begin(FCV_STAGE_FF1, l, s));
     for (int rep = m->launches(FCV_STAGE_FF1, l); rep > 0; --rep)
-      FCV_HIP(fcv::gemm_bias_gelu_bf16(nbuf, D, B(w.ff1_w) + (long)l * F * D, D,
-                                       folded ? fl + 6 * D + F : w.ff1_b + (long)l * F, R, F, D,
-                                       u, F, s, live_rows, folded ? fl + 6 * D : nullptr,
-                                       folded ? hstat : nullptr));
+      FCV_HIP(fcv::gemm_bias_gelu_f16(nbuf, D, B(w.ff1_w) + (long)l * F * D, D,
+                                      w.ff1_b + (long)l * F, R, F, D, u, F, s, live_rows));
     FCV_HIP(m->probe_end(FCV_STAGE_FF1, l, s));
-    // the next block's attention LayerNorm folds into this gated residual (not after the last)
-    const bool fold_next = folded && l + 1 < d.depth;
     FCV_HIP(m->probe_begin(FCV_STAGE_FF2, l, s));
     FCV_HIP(fcv::gemm_gated_residual(u, F, B(w.ff2_w) + (long)l * D * F, F,
                                      w.ff2_b + (long)l * D, R, D, F, h, D, mod + base + 5 * D,
-                                     mod_stride, docid, s, live_rows,
-                                     fold_next ? mod + base + 6 * D + D : nullptr, nbuf, hstat));
+                                     mod_stride, docid, s, live_rows));
     FCV_HIP(m->probe_end(FCV_STAGE_FF2, l, s));
   }
 
@@ -446,7 +409,7 @@ int fcv_dit_plan_capacity(FcvDit* m, const int32_t* cu_host, int32_t n_docs, int
                 " documents exceeds the capacity (" + std::to_string(rows_cap) + " rows, " +
                 std::to_string(docs_cap) + " documents)");
   // the kernels address activations by 32-bit byte offsets within buffer ranges held as an
-  // int: the widest row (the FF hidden row in bf16 or the fp32 residual row) times the internal
+  // int: the widest row (the FF hidden row in f16 or the fp32 residual row) times the internal
   // rows of the capacity must stay below 2 GB
   const long row_bytes = std::max<long>(2L * m->dims.ff_dim, 4L * m->dims.dim);
   FCV_CHECK(align_up(internal_rows_bound(rows_cap, docs_cap), kRowTile) * row_bytes < (1L << 31),
@@ -567,7 +530,7 @@ int fcv_dit_forward(FcvDit* m, const float* x, const float* mu, const float* con
             "spks and cond are required (null input pointer)");
   FCV_CHECK(n_t == 1 || n_t == m->n_docs, FCV_ERR_INVALID, "n_t must be 1 or n_docs");
   m->probe_count = 0;
-  return run_forward(m, x, mu, cond, spks, t, n_t, nullptr, nullptr, v_out, s);
+  return run_forward(m, x, mu, cond, spks, t, n_t, nullptr, v_out, s);
 }
 
 static int check_cfg_layout(const FcvDit* m) {
@@ -612,18 +575,14 @@ int solve_loop(FcvDit* m, float* x, const float* mu, const float* cond, const fl
   auto body = [&]() -> int {
     m->probe_count = 0;
     const float* mod = sched ? reinterpret_cast<const float*>(sched + S.mod) : m->at<float>(m->L.mod);
-    const float* fold =
-        sched ? reinterpret_cast<const float*>(sched + S.fold) : m->at<float>(m->L.fold);
     for (int step = 0; step < n_steps; ++step) {
       // every kModGroup steps, one pass over the AdaLN weights gives the next steps' rows
       if (!sched && step % kModGroup == 0) {
-        int r = compute_modulations(m, tbuf + step, std::min(kModGroup, n_steps - step), true,
-                                    s);
+        int r = compute_modulations(m, tbuf + step, std::min(kModGroup, n_steps - step), s);
         if (r != FCV_OK) return r;
       }
       const int row = sched ? step : step % kModGroup;
-      int r = run_forward(m, x, mu, cond, spks, nullptr, 1, mod + row * m->mod_width,
-                          fold + row * fold_width(m->dims), vbuf, s);
+      int r = run_forward(m, x, mu, cond, spks, nullptr, 1, mod + row * m->mod_width, vbuf, s);
       if (r != FCV_OK) return r;
       FCV_HIP(m->probe_begin(FCV_STAGE_EULER, -1, s));
       FCV_HIP(fcv::euler_cfg_update(x, vbuf, m->rc_cap, mel, dt_host[step], cfg, s,
@@ -718,13 +677,11 @@ int fcv_dit_schedule(FcvDit* m, const float* t_host, int32_t n_steps, void* sche
   char* b = static_cast<char*>(sched);
   float* t = reinterpret_cast<float*>(b + S.t);
   FCV_HIP(hipMemcpyAsync(t, t_host, n_steps * sizeof(float), hipMemcpyHostToDevice, s));
-  const long fw = fold_width(m->dims);
   for (int step = 0; step < n_steps; step += kModGroup) {
     int r = modulation_rows(m, t + step, std::min(kModGroup, n_steps - step),
-                            reinterpret_cast<bf16*>(b + S.tsin), reinterpret_cast<bf16*>(b + S.t1),
-                            reinterpret_cast<bf16*>(b + S.t2),
-                            reinterpret_cast<float*>(b + S.mod) + step * m->mod_width,
-                            reinterpret_cast<float*>(b + S.fold) + step * fw, s);
+                            reinterpret_cast<f16*>(b + S.tsin), reinterpret_cast<f16*>(b + S.t1),
+                            reinterpret_cast<f16*>(b + S.t2),
+                            reinterpret_cast<float*>(b + S.mod) + step * m->mod_width, s);
     if (r != FCV_OK) return r;
   }
   return FCV_OK;

@@ -1,7 +1,7 @@
 // Shared device helpers for the gfx950 DiT estimator kernels.
 //
 // Conventions used by every kernel in this library:
-//   * bf16 tensors are stored as raw 16-bit words (type `bf16` below);
+//   * GEMM operands, attention operands and the weights are IEEE fp16 (type `f16` below);
 //   * the residual stream and all boundary tensors are fp32;
 //   * MFMA fragments follow the CDNA 16x16 / 32x32 accumulator layouts:
 //       16x16x32 : lane l holds D[4*(l/16) + j][l%16], j = 0..3
@@ -15,22 +15,37 @@
 
 namespace fcv {
 
-typedef __bf16 bf16;
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kWave = 64;
 
-__device__ __forceinline__ float bf2f(bf16 v) { return (float)v; }
-__device__ __forceinline__ bf16 f2bf(float v) { return (bf16)v; }
+__device__ __forceinline__ float h2f(f16 v) { return (float)v; }
 
-__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+// fp32 -> fp16 conversions, round to nearest even from the fp32 values as computed.  The empty
+// asm pins those values: left to itself the backend fuses a product that feeds a conversion
+// into v_fma_mix, which rounds the exact product once instead of twice, and it does so in some
+// template instantiations and not in others, so an output's bits would depend on the GEMM tile
+// shape (and so on the batch a document is packed with).  The asm emits no instruction.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f16x2 f2h2(float a, float b) {
+  asm("" : "+v"(a), "+v"(b));
+  return f16x2{(f16)a, (f16)b};
 }
-__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f16 f2h(float v) { return f2h2(v, v)[0]; }
+__device__ __forceinline__ f16x4 f2h4(float a, float b, float c, float d) {
+  const f16x2 lo = f2h2(a, b), hi = f2h2(c, d);
+  return f16x4{lo[0], lo[1], hi[0], hi[1]};
+}
+
+__device__ __forceinline__ f32x4 mfma16(const f16x8& a, const f16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(const f16x8& a, const f16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -15,7 +15,7 @@ namespace {
 
 constexpr int TM = 128;       // output rows per workgroup
 constexpr int CG = 64;        // channels per group
-constexpr int LDP = CG + 8;   // padded LDS row (bf16): 16 consecutive rows hit distinct banks
+constexpr int LDP = CG + 8;   // padded LDS row (f16): 16 consecutive rows hit distinct banks
 constexpr int MAX_TAPS = 31;
 constexpr int WIN = TM + MAX_TAPS - 1;
 constexpr int SPITCH = CG + 4;  // fp32 staging row
@@ -28,18 +28,18 @@ constexpr int SMEM_BYTES = X_BYTES + W_BYTES > STAGE_BYTES ? X_BYTES + W_BYTES :
 // operand, so lane l accumulates output row l % 32 and, in register group g of channel tile t,
 // channels 32 t + 8 g + 4 (l / 32) + 0..3.  The epilogue stages each wave's 32 x 64 block
 // through LDS and reads it back row-major (16 lanes per row), so stores are contiguous runs of
-// 128 B (bf16 out) or 256 B (fp32 residual); the residual form issues all its h loads before
+// 128 B (f16 out) or 256 B (fp32 residual); the residual form issues all its h loads before
 // its first store.
-__global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x, int C,
-                                                      const bf16* __restrict__ w,
+__global__ __launch_bounds__(256, 2) void conv_kernel(const f16* __restrict__ x, int C,
+                                                      const f16* __restrict__ w,
                                                       const float* __restrict__ bias, int taps,
                                                       const int32_t* __restrict__ pos, int rows,
-                                                      bf16* __restrict__ out_bf16,
+                                                      f16* __restrict__ out_f16,
                                                       float* __restrict__ h,
                                                       const int32_t* __restrict__ rows_live) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM_BYTES];
-  bf16 (*sX)[LDP] = reinterpret_cast<bf16 (*)[LDP]>(smem);
-  bf16 (*sW)[CG][LDP] = reinterpret_cast<bf16 (*)[CG][LDP]>(smem + X_BYTES);
+  f16 (*sX)[LDP] = reinterpret_cast<f16 (*)[LDP]>(smem);
+  f16 (*sW)[CG][LDP] = reinterpret_cast<f16 (*)[CG][LDP]>(smem + X_BYTES);
 
   if (rows_live) rows = *rows_live;  // live rows of a capacity-sized grid
   const int m0 = blockIdx.x * TM;
@@ -54,21 +54,21 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
   const int chunk_c = (tid & 7) * 8;
   for (int r = tid >> 3; r < TM + halo; r += 32) {
     int src = min(max(m0 - halo + r, 0), rows - 1);
-    *reinterpret_cast<bf16x8*>(&sX[r][chunk_c]) =
-        *reinterpret_cast<const bf16x8*>(x + (long)src * C + g * CG + chunk_c);
+    *reinterpret_cast<f16x8*>(&sX[r][chunk_c]) =
+        *reinterpret_cast<const f16x8*>(x + (long)src * C + g * CG + chunk_c);
   }
 
-  const bf16* wg = w + (long)g * taps * CG * CG;
+  const f16* wg = w + (long)g * taps * CG * CG;
   const int lw_r = tid >> 3;  // 0..31
-  auto fetch = [&](bf16x8 (&rw)[2], int j) {
+  auto fetch = [&](f16x8 (&rw)[2], int j) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      rw[i] = *reinterpret_cast<const bf16x8*>(wg + ((long)j * CG + lw_r + 32 * i) * CG + chunk_c);
+      rw[i] = *reinterpret_cast<const f16x8*>(wg + ((long)j * CG + lw_r + 32 * i) * CG + chunk_c);
   };
-  auto stash = [&](const bf16x8 (&rw)[2], int buf) {
+  auto stash = [&](const f16x8 (&rw)[2], int buf) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      *reinterpret_cast<bf16x8*>(&sW[buf][lw_r + 32 * i][chunk_c]) = rw[i];
+      *reinterpret_cast<f16x8*>(&sW[buf][lw_r + 32 * i][chunk_c]) = rw[i];
   };
 
   // output row of this lane (B operand row) and its document position
@@ -84,17 +84,17 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[t][e] = 0.0f;
 
-  const bf16x8 zero8 = {};
+  const f16x8 zero8 = {};
   auto tap = [&](int j, int buf) {
     // rows before the row's document start read as zero (per-document causal padding)
     const bool live = lpos + j >= halo;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 v = *reinterpret_cast<const bf16x8*>(&sX[lrow + j][ks * 16 + fh * 8]);
-      const bf16x8 xb = live ? v : zero8;
+      const f16x8 v = *reinterpret_cast<const f16x8*>(&sX[lrow + j][ks * 16 + fh * 8]);
+      const f16x8 xb = live ? v : zero8;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const bf16x8 wa = *reinterpret_cast<const bf16x8*>(&sW[buf][t * 32 + fr][ks * 16 + fh * 8]);
+        const f16x8 wa = *reinterpret_cast<const f16x8*>(&sW[buf][t * 32 + fr][ks * 16 + fh * 8]);
         acc[t] = mfma32(wa, xb, acc[t]);
       }
     }
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
   // while tap j+2's loads are in flight, so a stash never waits on loads issued in its own tap
   // (a workgroup alone on its CU would otherwise wait out a load round trip every tap).  Taps
   // past the last re-read the last slice, so every path issues the same loads.
-  bf16x8 ra[2], rb[2];
+  f16x8 ra[2], rb[2];
   fetch(ra, 0);
   stash(ra, 0);
   fetch(ra, min(1, taps - 1));
@@ -153,22 +153,22 @@ __global__ __launch_bounds__(256, 2) void conv_kernel(const bf16* __restrict__ x
       const float4 r4 = {hv[p].x + y.x, hv[p].y + y.y, hv[p].z + y.z, hv[p].w + y.w};
       if (row < rows) *reinterpret_cast<float4*>(h + (long)row * C + col) = r4;
     } else {
-      const bf16x4 yb = {f2bf(y.x), f2bf(y.y), f2bf(y.z), f2bf(y.w)};
-      if (row < rows) *reinterpret_cast<bf16x4*>(out_bf16 + (long)row * C + col) = yb;
+      const f16x4 yb = f2h4(y.x, y.y, y.z, y.w);
+      if (row < rows) *reinterpret_cast<f16x4*>(out_f16 + (long)row * C + col) = yb;
     }
   }
 }
 
 }  // namespace
 
-hipError_t conv_causal_mish(const bf16* x, int C, const bf16* w, const float* bias, int taps,
-                            const int32_t* pos, int rows, bf16* out_bf16, float* h,
+hipError_t conv_causal_mish(const f16* x, int C, const f16* w, const float* bias, int taps,
+                            const int32_t* pos, int rows, f16* out_f16, float* h,
                             hipStream_t stream, const int32_t* rows_live) {
   if (rows <= 0) return hipSuccess;
   if (taps < 1 || taps > MAX_TAPS || C % CG != 0) return hipErrorInvalidValue;
   dim3 grid((rows + TM - 1) / TM, C / CG);
   hipLaunchKernelGGL(conv_kernel, grid, dim3(256), 0, stream, x, C, w, bias, taps, pos, rows,
-                     out_bf16, h, rows_live);
+                     out_f16, h, rows_live);
   return hipGetLastError();
 }
 

@@ -7,7 +7,7 @@ namespace fcv {
 namespace {
 
 // One wave per R consecutive rows; each lane owns C/256 float4 groups at stride 256 columns, so
-// every load/store instruction of the wave covers a contiguous 1 KB (fp32) / 512 B (bf16) span.
+// every load/store instruction of the wave covers a contiguous 1 KB (fp32) / 512 B (f16) span.
 // The loads of all R rows are issued before any arithmetic (R KB in flight per wave).  When
 // every document shares one modulation row (mod_stride == 0) shift and scale are read once per
 // wave instead of once per row.  Two-pass statistics from registers (mean, then centered
@@ -18,7 +18,7 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float* __restrict__ h
                                                      long mod_stride, int shift_off,
                                                      int scale_off,
                                                      const int32_t* __restrict__ docid,
-                                                     bf16* __restrict__ out,
+                                                     f16* __restrict__ out,
                                                      const int32_t* __restrict__ rows_live) {
   constexpr int G = C / 256;
   const int lane = threadIdx.x & 63;
@@ -59,14 +59,14 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const float* __restrict__ h
     }
     const float rstd = rsqrtf(wave_sum(ss) * (1.0f / C) + 1e-6f);
     if (mod_stride != 0) load_mod(row);
-    bf16x4* dst = reinterpret_cast<bf16x4*>(out + (long)row * C);
+    f16x4* dst = reinterpret_cast<f16x4*>(out + (long)row * C);
 #pragma unroll
     for (int i = 0; i < G; ++i) {
       const float4 x = v[r][i];
-      dst[lane + 64 * i] = bf16x4{f2bf((x.x - mean) * rstd * sc[i].x + sh[i].x),
-                                  f2bf((x.y - mean) * rstd * sc[i].y + sh[i].y),
-                                  f2bf((x.z - mean) * rstd * sc[i].z + sh[i].z),
-                                  f2bf((x.w - mean) * rstd * sc[i].w + sh[i].w)};
+      dst[lane + 64 * i] = f2h4(fmaf((x.x - mean) * rstd, sc[i].x, sh[i].x),
+                                fmaf((x.y - mean) * rstd, sc[i].y, sh[i].y),
+                                fmaf((x.z - mean) * rstd, sc[i].z, sh[i].z),
+                                fmaf((x.w - mean) * rstd, sc[i].w, sh[i].w));
     }
   }
 }
@@ -108,7 +108,7 @@ __global__ void pack_inputs_kernel(const float* __restrict__ x, const float* __r
                                    const float* __restrict__ mu, const float* __restrict__ spks,
                                    const int32_t* __restrict__ docid,
                                    const int32_t* __restrict__ ext_row, int rows, int mel,
-                                   bf16* __restrict__ a, const int32_t* __restrict__ rows_live) {
+                                   f16* __restrict__ a, const int32_t* __restrict__ rows_live) {
   if (rows_live) rows = *rows_live;
   const int per_row = (4 * mel) / 8;
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -117,7 +117,7 @@ __global__ void pack_inputs_kernel(const float* __restrict__ x, const float* __r
   const int c = (int)(idx % per_row) * 8;
   const int seg = c / mel, off = c % mel;
   const int e = ext_row[r];
-  bf16x8 o = {};
+  f16x8 o = {};
   if (e >= 0) {
     const float* src;
     if (seg == 0) src = x + (long)e * mel;
@@ -126,13 +126,14 @@ __global__ void pack_inputs_kernel(const float* __restrict__ x, const float* __r
     else src = spks + (long)docid[r] * mel;
     const float4 u = *reinterpret_cast<const float4*>(src + off);
     const float4 w = *reinterpret_cast<const float4*>(src + off + 4);
-    o = bf16x8{f2bf(u.x), f2bf(u.y), f2bf(u.z), f2bf(u.w), f2bf(w.x), f2bf(w.y), f2bf(w.z), f2bf(w.w)};
+    const f16x4 lo = f2h4(u.x, u.y, u.z, u.w), hi = f2h4(w.x, w.y, w.z, w.w);
+    o = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
-  *reinterpret_cast<bf16x8*>(a + (long)r * 4 * mel + c) = o;
+  *reinterpret_cast<f16x8*>(a + (long)r * 4 * mel + c) = o;
 }
 
 __global__ void sinusoid_kernel(const float* __restrict__ t, int n_t, int dim,
-                                bf16* __restrict__ out) {
+                                f16* __restrict__ out) {
   const int m = blockIdx.x;
   const int half = dim / 2;
   const float step = (float)(9.210340371976184 / (double)(half - 1));  // ln(1e4)/(half-1)
@@ -140,8 +141,8 @@ __global__ void sinusoid_kernel(const float* __restrict__ t, int n_t, int dim,
   for (int i = threadIdx.x; i < half; i += blockDim.x) {
     const float f = expf((float)i * -step);
     const float arg = scaled_t * f;
-    out[(long)m * dim + i] = f2bf(sinf(arg));
-    out[(long)m * dim + half + i] = f2bf(cosf(arg));
+    out[(long)m * dim + i] = f2h(sinf(arg));
+    out[(long)m * dim + half + i] = f2h(cosf(arg));
   }
 }
 
@@ -187,7 +188,7 @@ inline unsigned blocks_for(long n, int threads) { return (unsigned)((n + threads
 }  // namespace
 
 hipError_t layer_norm_modulate(const float* h, int C, int rows, const float* mod, long mod_stride,
-                               int shift_off, int scale_off, const int32_t* docid, bf16* out,
+                               int shift_off, int scale_off, const int32_t* docid, f16* out,
                                hipStream_t stream, const int32_t* rows_live) {
   if (rows <= 0) return hipSuccess;
   if (C != 1024) return hipErrorInvalidValue;
@@ -216,7 +217,7 @@ hipError_t build_aligned_row_index(const int32_t* cu_int, const int32_t* lens,
 }
 
 hipError_t pack_inputs(const float* x, const float* cond, const float* mu, const float* spks,
-                       const int32_t* docid, const int32_t* ext_row, int rows, int mel, bf16* a,
+                       const int32_t* docid, const int32_t* ext_row, int rows, int mel, f16* a,
                        hipStream_t stream, const int32_t* rows_live) {
   if (rows <= 0) return hipSuccess;
   if (mel % 8 != 0) return hipErrorInvalidValue;
@@ -226,7 +227,7 @@ hipError_t pack_inputs(const float* x, const float* cond, const float* mu, const
   return hipGetLastError();
 }
 
-hipError_t timestep_sinusoid(const float* t, int n_t, int dim, bf16* out, hipStream_t stream) {
+hipError_t timestep_sinusoid(const float* t, int n_t, int dim, f16* out, hipStream_t stream) {
   if (n_t <= 0) return hipSuccess;
   hipLaunchKernelGGL(sinusoid_kernel, dim3(n_t), dim3(128), 0, stream, t, n_t, dim, out);
   return hipGetLastError();

@@ -1,8 +1,8 @@
-// bf16 MFMA GEMM for gfx950 with fused epilogues.
+// f16 MFMA GEMM for gfx950 with fused epilogues.
 //
 // C[M,N] = A[M,K] . W[N,K]^T, both operands K-contiguous (PyTorch Linear layout), fp32
-// accumulation on v_mfma_f32_32x32x16_bf16 (on this part the 32x32x16 form sustains ~93% of
-// the bf16 peak in a register loop, the 16x16x32 form ~54%).
+// accumulation on v_mfma_f32_32x32x16_f16 (on this part the 32x32x16 form sustains ~93% of
+// the f16 peak in a register loop, the 16x16x32 form ~54%).
 //
 // Main loop.  A workgroup of WM x WN waves owns a BM x BN tile (256x256, 192x256, 128x256 and
 // 256x128 with 8 waves, 160x256, 128x128, 96x128 and 32x128 with 4 waves, several workgroups
@@ -23,15 +23,8 @@
 // Operand roles are swapped: the MFMA computes D = W_tile . A_tile^T, so the accumulator of a
 // 32x32 tile holds, in lane l, output row m = l % 32 and four consecutive output columns per
 // register group.  Every epilogue therefore reads and writes 4 consecutive columns of one row
-// at a time (16-byte fp32 / 8-byte bf16 vector accesses), and the interleaved RoPE pairs
+// at a time (16-byte fp32 / 8-byte f16 vector accesses), and the interleaved RoPE pairs
 // (2i, 2i+1) sit in the same lane.
-//
-// LayerNorm fold (kFold): the A operand is bf16(x * g) for a residual row x and the next
-// LayerNorm's scale row g, written by the gated-residual epilogue that produced x together with
-// per-row statistics of x in 32-column chunks.  The prologue combines each of the tile's rows'
-// chunks into (rs, -mu * rs) in LDS; the epilogue turns the accumulator into
-// rs * acc - mu * rs * u[col] (u = W . g), and the epilogue's bias is W . shift + bias.  That is
-// LN(x) * g + shift projected by W, without the normalized rows ever reaching memory.
 //
 // Rasterization: blocks are dealt round-robin over the 8 XCDs, so block ids are first remapped
 // to give each XCD a contiguous range of tiles; inside that range tiles are visited in groups of
@@ -48,7 +41,7 @@ namespace {
 constexpr int kXcds = 8;
 
 // Tile shape.  WM x WN waves; each wave owns (BM/WM) x (BN/WN) outputs as TM x TN MFMA tiles of
-// 32x32.  A ring of STAGES LDS slices of (BM + BN) x BK bf16; one wave-level copy fills 1 KB =
+// 32x32.  A ring of STAGES LDS slices of (BM + BN) x BK f16; one wave-level copy fills 1 KB =
 // ROWS_PER_COPY rows of one slice.
 template <int BM_, int BN_, int WM_, int WN_, int BK_ = 64, int STAGES_ = 2>
 struct TileCfg {
@@ -136,51 +129,6 @@ __device__ __forceinline__ void wait_loads_ahead(int ahead) {
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
-// The fold's inputs: per-row chunk statistics (kStatChunks x (sum, centered sum of squares))
-// and u = W . g per output column.
-struct FoldArgs {
-  const float2* stats;
-  const float* u;
-};
-
-// v from the lane a DPP control names (bound_ctrl off: every source lane exists here)
-template <int kCtrl>
-__device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
-}
-// sums over aligned groups of 8 and 16 lanes: two quad swaps, the half-row mirror (lane i adds
-// lane 7 - i, which holds the other quad's sum) and the row mirror (lane i adds lane 15 - i);
-// every lane of a group ends with the same value
-__device__ __forceinline__ float sum8(float v) {
-  v += dpp<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-  v += dpp<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-  v += dpp<0x141>(v);  // row_half_mirror
-  return v;
-}
-__device__ __forceinline__ float sum16(float v) {
-  const float h = sum8(v);
-  return h + dpp<0x140>(h);  // row_mirror
-}
-
-// (rs, -mu * rs) of one row from its chunk statistics, spread over an aligned group of 16 lanes
-// (lane j holds chunks 2j and 2j+1 as (sum, M2, sum, M2)): Chan et al.'s pairwise update
-// M2 = sum_c (M2_c + n_c (mean_c - mean)^2), eps 1e-6, biased variance.  Every lane of the
-// group gets the result.
-__device__ __forceinline__ float2 row_affine(const float4& c) {
-  constexpr float kN = 32.0f * kStatChunks;
-  const float mu = sum16(c.x + c.z) * (1.0f / kN);
-  const float d0 = c.x - 32.0f * mu, d1 = c.z - 32.0f * mu;
-  const float m2 = sum16((c.y + d0 * d0 * (1.0f / 32.0f)) + (c.w + d1 * d1 * (1.0f / 32.0f)));
-  const float rs = rsqrtf(m2 * (1.0f / kN) + 1e-6f);
-  return float2{rs, -mu * rs};
-}
-
-// rs * acc + (-mu * rs * u + bias): the folded LayerNorm and the epilogue's bias
-__device__ __forceinline__ float4 fold4(const f32x4& v, float2 a, const float4& u, const float4& b) {
-  return float4{fmaf(a.x, v[0], fmaf(a.y, u.x, b.x)), fmaf(a.x, v[1], fmaf(a.y, u.y, b.y)),
-                fmaf(a.x, v[2], fmaf(a.y, u.z, b.z)), fmaf(a.x, v[3], fmaf(a.y, u.w, b.w))};
-}
-
 // Whether an epilogue's per-row loads are issued one 32-row block ahead (the default); an
 // epilogue sets kPipelineRows = false when two blocks of its row context do not fit in registers.
 template <class E, class = void>
@@ -189,20 +137,15 @@ template <class E>
 struct pipeline_rows<E, std::void_t<decltype(E::kPipelineRows)>>
     : std::bool_constant<E::kPipelineRows> {};
 
-template <class C, class Epi, bool kFold>
+template <class C, class Epi>
 __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
-    const bf16* __restrict__ A, int lda, const bf16* __restrict__ W, int ldw, int M, int N, int K,
-    Epi epi, const int32_t* __restrict__ m_live, FoldArgs fold) {
+    const f16* __restrict__ A, int lda, const f16* __restrict__ W, int ldw, int M, int N, int K,
+    Epi epi, const int32_t* __restrict__ m_live) {
   constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN, BK = C::BK, S = C::STAGES;
-  // fold: 16 lanes per row's statistics, kStatRows rows per pass of the workgroup
-  constexpr int kStatRows = C::kThreads / 16;
-  constexpr int kStatPasses = kFold ? (BM + kStatRows - 1) / kStatRows : 1;
-  static_assert(kStatChunks == 32, "16 lanes x 2 chunks per row");
   // operand ring; after the K loop the same bytes stage the epilogue
-  __shared__ __attribute__((aligned(1024))) bf16 smem[S * (BM + BN) * BK];
-  __shared__ float2 rstat[kFold ? BM : 1];  // (rs, -mu * rs) of the tile's rows
-  bf16 (*sA)[BM * BK] = reinterpret_cast<bf16 (*)[BM * BK]>(smem);
-  bf16 (*sB)[BN * BK] = reinterpret_cast<bf16 (*)[BN * BK]>(smem + S * BM * BK);
+  __shared__ __attribute__((aligned(1024))) f16 smem[S * (BM + BN) * BK];
+  f16 (*sA)[BM * BK] = reinterpret_cast<f16 (*)[BM * BK]>(smem);
+  f16 (*sB)[BN * BK] = reinterpret_cast<f16 (*)[BN * BK]>(smem + S * BM * BK);
 
   if (m_live) M = *m_live;  // live rows of a capacity-sized grid
   const int tiles_n = N / BN;
@@ -212,25 +155,13 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   const int m0 = tmi * BM;
   const int n0 = tni * BN;
   const int lane = threadIdx.x & 63;
-  // fold: the tile's rows' chunk statistics (rows past M take row M - 1's, as the A copies do),
-  // fetched ahead of the operand copies so the wait for the first slice covers them; a pass
-  // reads kStatRows consecutive rows as one contiguous span
-  // per-row epilogue inputs (row_info) of the tile's rows, fetched with the statistics and
-  // parked in LDS with the first slice
+  // per-row epilogue inputs (row_info) of the tile's rows, fetched ahead of the operand copies
+  // (so the wait for the first slice covers them) and parked in LDS with the first slice
   static_assert(BM <= C::kThreads, "one thread per tile row");
   __shared__ int32_t rinfo[Epi::kRowInfo ? BM : 1];
   int rin = -1;
   if constexpr (Epi::kRowInfo) {
     if ((int)threadIdx.x < BM && m0 + (int)threadIdx.x < M) rin = epi.row_info(m0 + threadIdx.x);
-  }
-  float4 stat_in[kStatPasses];
-  if constexpr (kFold) {
-#pragma unroll
-    for (int p = 0; p < kStatPasses; ++p) {
-      const int r = min(p * kStatRows + (int)threadIdx.x / 16, BM - 1);
-      stat_in[p] = reinterpret_cast<const float4*>(
-          fold.stats + (long)min(m0 + r, M - 1) * kStatChunks)[threadIdx.x & 15];
-    }
   }
   // wave index as a scalar, so the copies' LDS destinations are computed in SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -259,8 +190,8 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   const uint32_t lds_a = lds_base + (uint32_t)wave * C::A_INSTR * kCopyBytes;
   const uint32_t lds_b = lds_base + S * BM * BK * 2 + (uint32_t)wave * C::B_INSTR * kCopyBytes;
   auto issue = [&](int kt, int stage) {
-    const bf16* a_k = A + kt * BK;
-    const bf16* w_k = W + kt * BK;
+    const f16* a_k = A + kt * BK;
+    const f16* w_k = W + kt * BK;
 #pragma unroll
     for (int i = 0; i < C::A_INSTR; ++i)
       lds_dma16(a_k, a_off[i], lds_a + stage * (BM * BK * 2) + i * kCopyBytes);
@@ -282,7 +213,6 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   const int rc = (lane % LANES_PER_ROW) * 4;
   Col scol{};
   Col dcol[TN][4];
-  float4 sfold{};
   if (direct) {
 #pragma unroll
     for (int j = 0; j < TN; ++j)
@@ -290,7 +220,6 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
       for (int g = 0; g < 4; ++g) dcol[j][g] = epi.column(col_base + j * 32 + g * 8 + (lane >> 5) * 4);
   } else {
     scol = epi.column(col_base + rc);
-    if constexpr (kFold) sfold = ld4(fold.u + col_base + rc);
   }
 
   f32x16 acc[TM][TN];
@@ -315,20 +244,20 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   const int KT = K / BK;
   constexpr int KS = BK / 16;
   static_assert(KS % 2 == 0, "k-step 0 of a slice uses fragment buffer 0");
-  bf16x8 fa[2][TM], fb[2][TN];
+  f16x8 fa[2][TM], fb[2][TN];
   auto load = [&](int buf, int ks, int st) {
-    const bf16* a_st = sA[st];
-    const bf16* b_st = sB[st];
+    const f16* a_st = sA[st];
+    const f16* b_st = sB[st];
     const int chunk = ks * 2 + fh;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int row = wm0 + i * 32 + fr;
-      fa[buf][i] = *reinterpret_cast<const bf16x8*>(a_st + row * BK + swz<BK>(row, chunk) * 8);
+      fa[buf][i] = *reinterpret_cast<const f16x8*>(a_st + row * BK + swz<BK>(row, chunk) * 8);
     }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int row = wn0 + j * 32 + fr;
-      fb[buf][j] = *reinterpret_cast<const bf16x8*>(b_st + row * BK + swz<BK>(row, chunk) * 8);
+      fb[buf][j] = *reinterpret_cast<const f16x8*>(b_st + row * BK + swz<BK>(row, chunk) * 8);
     }
   };
   // scheduling fences keep each k-step's LDS reads ahead of the previous k-step's MFMAs (left
@@ -354,14 +283,6 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   for (int st = 0; st < S - 1; ++st)
     if (st < KT) issue(st, st);
   wait_loads_ahead<C::LOADS, S - 2>(KT - 1);  // slice 0
-  if constexpr (kFold) {
-#pragma unroll
-    for (int p = 0; p < kStatPasses; ++p) {
-      const float2 a = row_affine(stat_in[p]);
-      const int r = p * kStatRows + (int)threadIdx.x / 16;
-      if ((threadIdx.x & 15) == 0 && r < BM) rstat[r] = a;
-    }
-  }
   if constexpr (Epi::kRowInfo) {
     if ((int)threadIdx.x < BM) rinfo[threadIdx.x] = rin;
   }
@@ -392,7 +313,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   // instruction would touch 32 rows.  Instead each wave stages one 32-row block at a time
   // through its own LDS region (row pitch padded by 16 bytes) and reads it back row-major:
   // lanes 16 r .. 16 r + 15 then cover TN x 32 consecutive columns of one row, so the epilogue's
-  // stores are contiguous runs of 16 x 16 B (fp32) or 16 x 8 B (bf16).  Epilogues that write a
+  // stores are contiguous runs of 16 x 16 B (fp32) or 16 x 8 B (f16).  Epilogues that write a
   // transposed layout (V^T) keep the direct lane layout, where 32 lanes cover 32 rows.
   // Row-dependent loads of a block (residual, row indices, rotary tables) are issued together
   // by prepare before the block's stores in finish; finish computes its values unconditionally
@@ -401,31 +322,18 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
   constexpr int PITCH = WCOLS + 4;  // floats
   static_assert(C::kWaves * 32 * PITCH * 4 <= (int)sizeof(smem), "epilogue staging");
   if (direct) {
-    // direct-layout tiles (V^T) read nothing per row; the fold's u columns are read here, one
-    // 32-column block at a time, not before the K loop, where they would stay live in registers
-    // through it (nothing has been stored yet, so these loads wait for nothing else)
+    // direct-layout tiles (V^T) read nothing per row
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      float4 ufold[kFold ? 4 : 1];
-      if constexpr (kFold) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) ufold[g] = ld4(fold.u + col_base + j * 32 + g * 8 + fh * 4);
-      }
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int row = m0 + wm0 + i * 32 + fr;
-        float2 aff{1.0f, 0.0f};
-        if constexpr (kFold) aff = rstat[wm0 + i * 32 + fr];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                            acc[i][j][4 * g + 3]};
           const int c = col_base + j * 32 + g * 8 + fh * 4;
-          if constexpr (kFold)
-            epi.finish_biased(fold4(v, aff, ufold[g], dcol[j][g].b), epi.blank(dcol[j][g]),
-                              dcol[j][g], row, c, M);
-          else
-            epi.finish(v, epi.blank(dcol[j][g]), dcol[j][g], row, c, M);
+          epi.finish(v, epi.blank(dcol[j][g]), dcol[j][g], row, c, M);
         }
       }
     }
@@ -488,11 +396,7 @@ __global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
       for (int p = 0; p < PASSES; ++p) {
         const int r = p * ROWS_PER_PASS + rr;
         const Ctx x = kLoads ? cx[p] : epi.blank(scol);
-        if constexpr (kFold)
-          epi.finish_biased(fold4(v[p], rstat[wm0 + i * 32 + r], sfold, scol.b), x, scol,
-                            m0 + wm0 + i * 32 + r, col, M);
-        else
-          epi.finish(v[p], x, scol, m0 + wm0 + i * 32 + r, col, M);
+        epi.finish(v[p], x, scol, m0 + wm0 + i * 32 + r, col, M);
       }
       if constexpr (kLoads && kAhead) {
         if (i + 1 < TM) {
@@ -544,15 +448,14 @@ __device__ __forceinline__ void buffer_st4(__amdgpu_buffer_rsrc_t r, uint32_t of
                    __float_as_uint(x.w)};
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
 }
-__device__ __forceinline__ void buffer_st_bf16x4(__amdgpu_buffer_rsrc_t r, uint32_t off, bf16x4 x) {
+__device__ __forceinline__ void buffer_st_f16x4(__amdgpu_buffer_rsrc_t r, uint32_t off, f16x4 x) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, x), r, off, 0, 0);
 }
 
-struct EpiBiasF32Bf16 {
-  static constexpr bool kFoldable = false;
+struct EpiBiasF32F16 {
   const float* bias;
   float* out_f32;
-  bf16* out_bf16;
+  f16* out_f16;
   int ldo;
   using Col = BiasCol;
   using Ctx = NoCtx;
@@ -564,15 +467,14 @@ struct EpiBiasF32Bf16 {
   __device__ Ctx prepare(int, int, int, const Col&, int) const { return {}; }
   __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
-    const bf16x4 yb = {f2bf(y.x), f2bf(y.y), f2bf(y.z), f2bf(y.w)};
+    const f16x4 yb = f2h4(y.x, y.y, y.z, y.w);
     if (row >= M) return;
     *reinterpret_cast<float4*>(out_f32 + (long)row * ldo + col) = y;
-    *reinterpret_cast<bf16x4*>(out_bf16 + (long)row * ldo + col) = yb;
+    *reinterpret_cast<f16x4*>(out_f16 + (long)row * ldo + col) = yb;
   }
 };
 
 struct EpiBiasF32 {
-  static constexpr bool kFoldable = false;
   const float* bias;
   float* out;
   int ldo;
@@ -595,7 +497,6 @@ struct EpiBiasF32 {
 };
 
 struct EpiBiasF32RowMap {
-  static constexpr bool kFoldable = false;
   const float* bias;
   float* out;
   int ldo;
@@ -621,10 +522,9 @@ struct EpiBiasF32RowMap {
   }
 };
 
-struct EpiBiasSiluBf16 {
-  static constexpr bool kFoldable = false;
+struct EpiBiasSiluF16 {
   const float* bias;
-  bf16* out;
+  f16* out;
   int ldo;
   using Col = BiasCol;
   using Ctx = NoCtx;
@@ -636,16 +536,15 @@ struct EpiBiasSiluBf16 {
   __device__ Ctx prepare(int, int, int, const Col&, int) const { return {}; }
   __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
-    const bf16x4 yb = {f2bf(silu(y.x)), f2bf(silu(y.y)), f2bf(silu(y.z)), f2bf(silu(y.w))};
+    const f16x4 yb = f2h4(silu(y.x), silu(y.y), silu(y.z), silu(y.w));
     if (row >= M) return;
-    *reinterpret_cast<bf16x4*>(out + (long)row * ldo + col) = yb;
+    *reinterpret_cast<f16x4*>(out + (long)row * ldo + col) = yb;
   }
 };
 
-struct EpiBiasGeluBf16 {
-  static constexpr bool kFoldable = true;  // FF1
+struct EpiBiasGeluF16 {
   const float* bias;
-  bf16* out;
+  f16* out;
   int ldo;
   using Col = BiasCol;
   using Ctx = NoCtx;
@@ -655,39 +554,25 @@ struct EpiBiasGeluBf16 {
   __device__ Col column(int col) const { return {ld4(bias + col)}; }
   static constexpr bool kRowInfo = false;
   __device__ Ctx prepare(int, int, int, const Col&, int) const { return {}; }
-  __device__ void finish(const f32x4& v, const Ctx& x, const Col& c, int row, int col, int M) const {
-    finish_biased(add4(v, c.b), x, c, row, col, M);
-  }
-  // y = acc + bias already (the LayerNorm fold adds the bias with its own terms)
-  __device__ void finish_biased(const float4& y, const Ctx&, const Col&, int row, int col,
-                                int M) const {
-    const bf16x4 yb = {f2bf(gelu_tanh(y.x)), f2bf(gelu_tanh(y.y)), f2bf(gelu_tanh(y.z)),
-                       f2bf(gelu_tanh(y.w))};
-    buffer_st_bf16x4(buffer_over(out, (uint32_t)M * ldo * 2), (uint32_t)(row * ldo + col) * 2, yb);
+  __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
+    const float4 y = add4(v, c.b);
+    const f16x4 yb = f2h4(gelu_tanh(y.x), gelu_tanh(y.y), gelu_tanh(y.z), gelu_tanh(y.w));
+    buffer_st_f16x4(buffer_over(out, (uint32_t)M * ldo * 2), (uint32_t)(row * ldo + col) * 2, yb);
   }
 };
 
 // h += gate * (acc + bias).  kPerDoc: each document has its own gate row (gate + d * mod_stride,
 // d = docid[row]); otherwise one gate row is shared by every document and is loaded with the
 // bias, before the K loop.  h is read and written through raw buffer accesses over its M rows.
-// kNext (shared gate rows only): also write the next LayerNorm fold's inputs for the new h:
-// anext = bf16(h * gnext) and, per row and 32-column chunk, (sum, centered sum of squares).
-// The 8 lanes holding a chunk's columns reduce it in a fixed order (sum8), so the statistics are
-// the same for every tile shape.
-template <bool kPerDoc, bool kNext>
+template <bool kPerDoc>
 struct EpiGatedResidual {
-  static constexpr bool kFoldable = false;
   const float* bias;
   float* h;
   int ldh;
   const float* gate;  // mod + gate offset
   long mod_stride;
   const int32_t* docid;
-  const float* gnext;  // next LayerNorm's scale row
-  bf16* anext;         // [M][ldh]
-  float2* stats;       // [M][kStatChunks]
-  static_assert(!(kPerDoc && kNext), "the fold needs one modulation row for every document");
-  struct Col { float4 b, g, gn; };
+  struct Col { float4 b, g; };
   struct Ctx { float4 g, x; };
   __device__ bool row_loads(int, int) const { return true; }
   __device__ Ctx blank(const Col& c) const { return {c.g, float4{0.f, 0.f, 0.f, 0.f}}; }
@@ -696,7 +581,6 @@ struct EpiGatedResidual {
     Col c;
     c.b = ld4(bias + col);
     c.g = kPerDoc ? float4{0.f, 0.f, 0.f, 0.f} : ld4(gate + col);
-    c.gn = kNext ? ld4(gnext + col) : float4{0.f, 0.f, 0.f, 0.f};
     return c;
   }
   static constexpr bool kRowInfo = kPerDoc;  // the row's document
@@ -714,25 +598,13 @@ struct EpiGatedResidual {
   }
   __device__ void finish(const f32x4& v, const Ctx& x, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
-    const float4 r = {x.x.x + x.g.x * y.x, x.x.y + x.g.y * y.y, x.x.z + x.g.z * y.z,
-                      x.x.w + x.g.w * y.w};
+    const float4 r = {fmaf(x.g.x, y.x, x.x.x), fmaf(x.g.y, y.y, x.x.y), fmaf(x.g.z, y.z, x.x.z),
+                      fmaf(x.g.w, y.w, x.x.w)};
     buffer_st4(buffer_over(h, (uint32_t)M * ldh * 4), (uint32_t)(row * ldh + col) * 4, r);
-    if constexpr (kNext) {
-      const bf16x4 a = {f2bf(r.x * c.gn.x), f2bf(r.y * c.gn.y), f2bf(r.z * c.gn.z),
-                        f2bf(r.w * c.gn.w)};
-      buffer_st_bf16x4(buffer_over(anext, (uint32_t)M * ldh * 2), (uint32_t)(row * ldh + col) * 2,
-                       a);
-      const float sum = sum8((r.x + r.y) + (r.z + r.w));
-      const float mc = sum * (1.0f / 32.0f);
-      const float d0 = r.x - mc, d1 = r.y - mc, d2 = r.z - mc, d3 = r.w - mc;
-      const float m2 = sum8((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3));
-      if ((threadIdx.x & 7) == 0 && row < M) stats[(long)row * kStatChunks + (col >> 5)] = float2{sum, m2};
-    }
   }
 };
 
 struct EpiQkvRope {
-  static constexpr bool kFoldable = true;
   const float* bias;
   int dim;        // heads * 64
   int rows;       // q / k row pitch per head (rp)
@@ -741,9 +613,9 @@ struct EpiQkvRope {
   const float* rope_sin;
   int rope_dim;
   int max_pos;
-  bf16* q;
-  bf16* k;
-  bf16* vt;
+  f16* q;
+  f16* k;
+  f16* vt;
   int rp;
   using Col = BiasCol;
   struct Ctx { float2 cs, sn; };
@@ -771,17 +643,14 @@ struct EpiQkvRope {
   }
   __device__ void finish(const f32x4& v, const Ctx& cx, const Col& cb, int row, int col,
                          int M) const {
-    finish_biased(add4(v, cb.b), cx, cb, row, col, M);
-  }
-  // y = acc + bias already (the LayerNorm fold adds the bias with its own terms)
-  __device__ void finish_biased(float4 y, const Ctx& cx, const Col&, int row, int col,
-                                int M) const {
+    float4 y = add4(v, cb.b);
     const int which = col / dim;  // 0 q, 1 k, 2 v
     const int c = col - which * dim;
     const int head = c >> 6, d = c & 63;
     if (which == 2) {
       // V transposed: vt[head][d + e][row]; rows in [M, rp) get finite copies of row M-1
-      const bf16 v0 = f2bf(y.x), v1 = f2bf(y.y), v2 = f2bf(y.z), v3 = f2bf(y.w);
+      const f16x4 v4 = f2h4(y.x, y.y, y.z, y.w);
+      const f16 v0 = v4[0], v1 = v4[1], v2 = v4[2], v3 = v4[3];
       if (row >= rp) return;
       vt[((long)head * 64 + d) * rp + row] = v0;
       vt[((long)head * 64 + d + 1) * rp + row] = v1;
@@ -795,10 +664,10 @@ struct EpiQkvRope {
     const float4 yr = {a0 * cx.cs.x - b0 * cx.sn.x, b0 * cx.cs.x + a0 * cx.sn.x,
                        a1 * cx.cs.y - b1 * cx.sn.y, b1 * cx.cs.y + a1 * cx.sn.y};
     if (c < rope_dim) y = yr;
-    const bf16x4 yb = {f2bf(y.x), f2bf(y.y), f2bf(y.z), f2bf(y.w)};
+    const f16x4 yb = f2h4(y.x, y.y, y.z, y.w);
     if (row >= M) return;
-    bf16* dst = (which == 0 ? q : k) + ((long)head * rows + row) * 64 + d;
-    *reinterpret_cast<bf16x4*>(dst) = yb;
+    f16* dst = (which == 0 ? q : k) + ((long)head * rows + row) * 64 + d;
+    *reinterpret_cast<f16x4*>(dst) = yb;
   }
 };
 
@@ -815,22 +684,12 @@ using Tile128x128x3 = TileCfg<128, 128, 2, 2, 64, 3>;  // one workgroup per CU
 using Tile32x128x4 = TileCfg<32, 128, 1, 4, 64, 4>;
 
 template <class C, class Epi>
-hipError_t launch_tile(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
-                       const Epi& epi, hipStream_t stream, const int32_t* m_live,
-                       const FoldArgs& fold) {
+hipError_t launch_tile(const f16* A, int lda, const f16* W, int ldw, int M, int N, int K,
+                       const Epi& epi, hipStream_t stream, const int32_t* m_live) {
   if (N % C::BN != 0 || K % C::BK != 0) return hipErrorInvalidValue;
   const int tiles = ((M + C::BM - 1) / C::BM) * (N / C::BN);
-  if constexpr (Epi::kFoldable) {
-    if (fold.u) {
-      hipLaunchKernelGGL((gemm_kernel<C, Epi, true>), dim3(tiles), dim3(C::kThreads), 0, stream,
-                         A, lda, W, ldw, M, N, K, epi, m_live, fold);
-      return hipGetLastError();
-    }
-  } else {
-    if (fold.u) return hipErrorInvalidValue;
-  }
-  hipLaunchKernelGGL((gemm_kernel<C, Epi, false>), dim3(tiles), dim3(C::kThreads), 0, stream, A,
-                     lda, W, ldw, M, N, K, epi, m_live, fold);
+  hipLaunchKernelGGL((gemm_kernel<C, Epi>), dim3(tiles), dim3(C::kThreads), 0, stream, A, lda, W,
+                     ldw, M, N, K, epi, m_live);
   return hipGetLastError();
 }
 
@@ -882,49 +741,46 @@ inline int forced_tile(int N) {
 // exceed it).  The tile shape is chosen from M; it never changes an element's K summation
 // order, so a layout's results are the same under any capacity.
 template <class Epi>
-hipError_t launch(const bf16* A, int lda, const bf16* W, int ldw, int M, int N, int K,
-                  const Epi& epi, hipStream_t stream, const int32_t* m_live = nullptr,
-                  const FoldArgs& fold = FoldArgs{nullptr, nullptr}) {
-  // the fold's statistics cover K = kStatChunks x 32 columns
-  if (fold.u && (!fold.stats || K != kStatChunks * 32)) return hipErrorInvalidValue;
+hipError_t launch(const f16* A, int lda, const f16* W, int ldw, int M, int N, int K,
+                  const Epi& epi, hipStream_t stream, const int32_t* m_live = nullptr) {
   if (M <= 0) return hipSuccess;
   if (N % 128 != 0 || K % 64 != 0 || lda % 8 != 0 || ldw % 8 != 0) return hipErrorInvalidValue;
   // the copies address A and W by 32-bit byte offsets from their bases
   if ((long)M * lda * 2 >= (1L << 32) || (long)N * ldw * 2 >= (1L << 32)) return hipErrorInvalidValue;
   const int forced = forced_tile(N);
   switch (forced >= 0 ? forced : choose_tile(M, N)) {
-    case 0: return launch_tile<Tile256x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
-    case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
-    case 2: return launch_tile<Tile128x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
-    case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+    case 0: return launch_tile<Tile256x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case 1: return launch_tile<Tile192x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case 2: return launch_tile<Tile128x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case 3: return launch_tile<Tile256x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
     case 5:
       if ((long)((M + 31) / 32) * (N / 128) <= kCus)
-        return launch_tile<Tile32x128x4>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
-      return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
-    case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+        return launch_tile<Tile32x128x4>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+      return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
     case 7:
       // where the tiles fit one round of CUs, a third ring stage gives each copy more lead (the
       // tile then holds a CU alone); with more tiles the two-stage form's two per CU win
       if ((long)((M + 95) / 96) * (N / 128) <= kCus)
-        return launch_tile<Tile96x128x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
-      return launch_tile<Tile96x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+        return launch_tile<Tile96x128x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+      return launch_tile<Tile96x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
     default:
       if ((long)((M + 127) / 128) * (N / 128) <= kCus)
-        return launch_tile<Tile128x128x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
-      return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live, fold);
+        return launch_tile<Tile128x128x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+      return launch_tile<Tile128x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
   }
 }
 
 }  // namespace
 
-hipError_t gemm_bias_f32_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
-                              int M, int N, int K, float* out_f32, bf16* out_bf16, int ldo,
+hipError_t gemm_bias_f32_f16(const f16* A, int lda, const f16* W, int ldw, const float* bias,
+                              int M, int N, int K, float* out_f32, f16* out_f16, int ldo,
                               hipStream_t stream, const int32_t* m_live) {
-  return launch(A, lda, W, ldw, M, N, K, EpiBiasF32Bf16{bias, out_f32, out_bf16, ldo}, stream,
+  return launch(A, lda, W, ldw, M, N, K, EpiBiasF32F16{bias, out_f32, out_f16, ldo}, stream,
                 m_live);
 }
 
-hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
+hipError_t gemm_bias_f32(const f16* A, int lda, const f16* W, int ldw, const float* bias,
                          int M, int N, int K, float* out, int ldo, int n_valid,
                          hipStream_t stream) {
   if (n_valid % 4 != 0) return hipErrorInvalidValue;
@@ -936,7 +792,7 @@ hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const f
   return launch(A, lda, W, ldw, M, N, K, EpiBiasF32{bias, out, ldo, n_valid}, stream);
 }
 
-hipError_t gemm_bias_f32_rowmap(const bf16* A, int lda, const bf16* W, int ldw,
+hipError_t gemm_bias_f32_rowmap(const f16* A, int lda, const f16* W, int ldw,
                                 const float* bias, int M, int N, int K, float* out, int ldo,
                                 int n_valid, const int32_t* row_map, hipStream_t stream,
                                 const int32_t* m_live) {
@@ -945,56 +801,41 @@ hipError_t gemm_bias_f32_rowmap(const bf16* A, int lda, const bf16* W, int ldw,
                 stream, m_live);
 }
 
-hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
-                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream) {
+hipError_t gemm_bias_silu_f16(const f16* A, int lda, const f16* W, int ldw, const float* bias,
+                               int M, int N, int K, f16* out, int ldo, hipStream_t stream) {
   if (gemv_supported(M, K, lda, ldw))
-    return gemv_bias_silu_bf16(A, lda, W, ldw, bias, M, N, K, out, ldo, stream);
-  return launch(A, lda, W, ldw, M, N, K, EpiBiasSiluBf16{bias, out, ldo}, stream);
+    return gemv_bias_silu_f16(A, lda, W, ldw, bias, M, N, K, out, ldo, stream);
+  return launch(A, lda, W, ldw, M, N, K, EpiBiasSiluF16{bias, out, ldo}, stream);
 }
 
-hipError_t gemm_bias_gelu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
-                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream,
-                               const int32_t* m_live, const float* fold_u,
-                               const float2* fold_stats) {
+hipError_t gemm_bias_gelu_f16(const f16* A, int lda, const f16* W, int ldw, const float* bias,
+                              int M, int N, int K, f16* out, int ldo, hipStream_t stream,
+                              const int32_t* m_live) {
   if ((long)M * ldo * 2 >= (1L << 31)) return hipErrorInvalidValue;  // buffer range is an int
-  return launch(A, lda, W, ldw, M, N, K, EpiBiasGeluBf16{bias, out, ldo}, stream, m_live,
-                FoldArgs{fold_stats, fold_u});
+  return launch(A, lda, W, ldw, M, N, K, EpiBiasGeluF16{bias, out, ldo}, stream, m_live);
 }
 
-hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
+hipError_t gemm_gated_residual(const f16* A, int lda, const f16* W, int ldw, const float* bias,
                                int M, int N, int K, float* h, int ldh, const float* gate,
                                long mod_stride, const int32_t* docid, hipStream_t stream,
-                               const int32_t* m_live, const float* gnext, bf16* anext,
-                               float2* stats) {
+                               const int32_t* m_live) {
   if ((long)M * ldh * 4 >= (1L << 31)) return hipErrorInvalidValue;  // buffer range is an int
-  if (gnext) {
-    if (mod_stride != 0 || !anext || !stats || N != kStatChunks * 32 || ldh % 4 != 0)
-      return hipErrorInvalidValue;
-    return launch(A, lda, W, ldw, M, N, K,
-                  EpiGatedResidual<false, true>{bias, h, ldh, gate, 0, docid, gnext, anext, stats},
-                  stream, m_live);
-  }
   if (mod_stride == 0)
     return launch(A, lda, W, ldw, M, N, K,
-                  EpiGatedResidual<false, false>{bias, h, ldh, gate, 0, docid, nullptr, nullptr,
-                                                 nullptr},
-                  stream, m_live);
+                  EpiGatedResidual<false>{bias, h, ldh, gate, 0, docid}, stream, m_live);
   return launch(A, lda, W, ldw, M, N, K,
-                EpiGatedResidual<true, false>{bias, h, ldh, gate, mod_stride, docid, nullptr,
-                                              nullptr, nullptr},
-                stream, m_live);
+                EpiGatedResidual<true>{bias, h, ldh, gate, mod_stride, docid}, stream, m_live);
 }
 
-hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const float* bias, int M,
+hipError_t gemm_qkv_rope(const f16* A, int lda, const f16* W, int ldw, const float* bias, int M,
                          int dim, int heads, const int32_t* pos, const float* rope_cos,
-                         const float* rope_sin, int rope_dim, int max_pos, bf16* q, bf16* k,
-                         bf16* vt, int rp, hipStream_t stream, const int32_t* m_live,
-                         const float* fold_u, const float2* fold_stats) {
+                         const float* rope_sin, int rope_dim, int max_pos, f16* q, f16* k,
+                         f16* vt, int rp, hipStream_t stream, const int32_t* m_live) {
   (void)heads;
   if (rp < M) return hipErrorInvalidValue;
   return launch(A, lda, W, ldw, M, 3 * dim, dim,
                 EpiQkvRope{bias, dim, rp, pos, rope_cos, rope_sin, rope_dim, max_pos, q, k, vt, rp},
-                stream, m_live, FoldArgs{fold_stats, fold_u});
+                stream, m_live);
 }
 
 }  // namespace fcv

@@ -16,83 +16,59 @@ namespace fcv {
 // Launchers given live == nullptr use their static count arguments.
 enum { kLiveRows = 0, kLiveTiles = 1, kLiveHalfRows = 2 };  // internal rows, attention tiles, rc
 
-// ---- LayerNorm folded into the next GEMM ----------------------------------------------
-// With one modulation row shared by every document, (LN(x) * g + shift) . W^T + bias is
-//   rs * (bf16(x * g) . W^T) - mu * rs * (W . g) + (W . shift + bias),
-// mu and rs = 1 / sqrt(var + 1e-6) the row's LayerNorm statistics.  The gated-residual GEMM
-// that produces x writes bf16(x * g) and, per row, kStatChunks chunks of 32 columns as
-// (sum, centered sum of squares); the next GEMM (fold_u = W . g, bias = W . shift + bias, both
-// from adaln_fold) combines the chunks in a fixed order.  Rows' statistics and products then
-// do not depend on the tile shape or on the batch.
-constexpr int kStatChunks = 32;  // the model width, 1024, in chunks of 32 columns
-
 // ---- GEMM: C[M,N] = A[M,K] . W[N,K]^T (+ bias) with a fused epilogue -------------------
 // Requirements checked by the caller: N % 128 == 0, K % 64 == 0, lda/ldw % 8 == 0.
 // M is the capacity the grid is sized for; m_live (when not null) holds the live row count
 // (<= M).
 
-// out_f32[r, c] = acc + bias[c];  out_bf16[r, c] = bf16(same)   (input projection)
-hipError_t gemm_bias_f32_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
-                              int M, int N, int K, float* out_f32, bf16* out_bf16, int ldo,
+// out_f32[r, c] = acc + bias[c];  out_f16[r, c] = f16(same)   (input projection)
+hipError_t gemm_bias_f32_f16(const f16* A, int lda, const f16* W, int ldw, const float* bias,
+                              int M, int N, int K, float* out_f32, f16* out_f16, int ldo,
                               hipStream_t stream, const int32_t* m_live = nullptr);
 
 // out[r, c] = acc + bias[c] for c < n_valid (fp32; AdaLN projection)
-hipError_t gemm_bias_f32(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
+hipError_t gemm_bias_f32(const f16* A, int lda, const f16* W, int ldw, const float* bias,
                          int M, int N, int K, float* out, int ldo, int n_valid, hipStream_t stream);
 
 // out[row_map[r], c] = acc + bias[c] for c < n_valid and row_map[r] >= 0 (proj_out)
-hipError_t gemm_bias_f32_rowmap(const bf16* A, int lda, const bf16* W, int ldw,
+hipError_t gemm_bias_f32_rowmap(const f16* A, int lda, const f16* W, int ldw,
                                 const float* bias, int M, int N, int K, float* out, int ldo,
                                 int n_valid, const int32_t* row_map, hipStream_t stream,
                                 const int32_t* m_live = nullptr);
 
-// out[r, c] = bf16(silu(acc + bias[c]))   (timestep MLP)
-hipError_t gemm_bias_silu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
-                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream);
+// out[r, c] = f16(silu(acc + bias[c]))   (timestep MLP)
+hipError_t gemm_bias_silu_f16(const f16* A, int lda, const f16* W, int ldw, const float* bias,
+                               int M, int N, int K, f16* out, int ldo, hipStream_t stream);
 
-// out[r, c] = bf16(gelu_tanh(acc + bias[c]))   (FF1).  With fold_u: the LayerNorm fold, acc
-// replaced by rs * acc - mu * rs * fold_u[c] from fold_stats (K must be kStatChunks * 32).
-hipError_t gemm_bias_gelu_bf16(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
-                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream,
-                               const int32_t* m_live = nullptr, const float* fold_u = nullptr,
-                               const float2* fold_stats = nullptr);
+// out[r, c] = f16(gelu_tanh(acc + bias[c]))   (FF1)
+hipError_t gemm_bias_gelu_f16(const f16* A, int lda, const f16* W, int ldw, const float* bias,
+                              int M, int N, int K, f16* out, int ldo, hipStream_t stream,
+                              const int32_t* m_live = nullptr);
 
 // h[r, c] += gate[c] * (acc + bias[c]), gate row = mod + docid[r] * mod_stride + gate_off
-// (out-projection and FF2 gated residuals).  With gnext (mod_stride 0, N = kStatChunks * 32):
-// also anext[r, c] = bf16(h[r, c] * gnext[c]) and stats[r][chunk], the next LayerNorm fold's
-// inputs.
-hipError_t gemm_gated_residual(const bf16* A, int lda, const bf16* W, int ldw, const float* bias,
+// (out-projection and FF2 gated residuals).
+hipError_t gemm_gated_residual(const f16* A, int lda, const f16* W, int ldw, const float* bias,
                                int M, int N, int K, float* h, int ldh, const float* mod,
                                long mod_stride, const int32_t* docid, hipStream_t stream,
-                               const int32_t* m_live = nullptr, const float* gnext = nullptr,
-                               bf16* anext = nullptr, float2* stats = nullptr);
+                               const int32_t* m_live = nullptr);
 
 // Fused QKV projection: bias, interleaved RoPE on columns [0, rope_dim) of q and k
 // (angles from cos/sin tables [max_pos][rope_dim/2], row position min(pos[r], max_pos-1)),
 // scatter to q, k : [heads][rp][dim_head] and vt : [heads][dim_head][rp] (V transposed).
-hipError_t gemm_qkv_rope(const bf16* A, int lda, const bf16* W, int ldw, const float* bias, int M,
+hipError_t gemm_qkv_rope(const f16* A, int lda, const f16* W, int ldw, const float* bias, int M,
                          int dim, int heads, const int32_t* pos, const float* rope_cos,
-                         const float* rope_sin, int rope_dim, int max_pos, bf16* q, bf16* k,
-                         bf16* vt, int rp, hipStream_t stream, const int32_t* m_live = nullptr,
-                         const float* fold_u = nullptr, const float2* fold_stats = nullptr);
+                         const float* rope_sin, int rope_dim, int max_pos, f16* q, f16* k,
+                         f16* vt, int rp, hipStream_t stream, const int32_t* m_live = nullptr);
 
 // ---- skinny products (few rows sharing W, K in {512, 1024}): bandwidth-bound, no MFMA -------
 // Launches of up to 16 rows each; a row's result is the same whatever M is.
 bool gemv_supported(int M, int K, int lda, int ldw);
 // out[m, n] = acc + bias[n]
-hipError_t gemv_bias_f32(const bf16* a, int lda, const bf16* W, int ldw, const float* bias, int M,
+hipError_t gemv_bias_f32(const f16* a, int lda, const f16* W, int ldw, const float* bias, int M,
                          int N, int K, float* out, int ldo, hipStream_t stream);
-// The LayerNorm fold's column terms for n_t modulation rows (row s at mod + s * mod_width) and
-// every block l < depth: fold + (s * depth + l) * (6 dim + 2 ff_dim) holds
-//   [W_qkv . g_att | W_qkv . shift_att + b_qkv | W_ff1 . g_ff | W_ff1 . shift_ff + b_ff1],
-// with (shift_att, g_att) at block offsets (0, dim) and (shift_ff, g_ff) at (3 dim, 4 dim) of
-// the block's 6 dim modulation columns.  fp32 dot products of the bf16 weights; dim 1024.
-hipError_t adaln_fold(const bf16* qkv_w, const float* qkv_b, const bf16* ff1_w,
-                      const float* ff1_b, int depth, int dim, int ff_dim, const float* mod,
-                      long mod_width, int n_t, float* fold, hipStream_t stream);
-// out[m, n] = bf16(silu(acc + bias[n]))
-hipError_t gemv_bias_silu_bf16(const bf16* a, int lda, const bf16* W, int ldw, const float* bias,
-                               int M, int N, int K, bf16* out, int ldo, hipStream_t stream);
+// out[m, n] = f16(silu(acc + bias[n]))
+hipError_t gemv_bias_silu_f16(const f16* a, int lda, const f16* W, int ldw, const float* bias,
+                               int M, int N, int K, f16* out, int ldo, hipStream_t stream);
 
 // ---- attention ----------------------------------------------------------------------------
 // Varlen attention, head_dim 64.  tiles (16-byte aligned) holds one 4-int entry per tile of
@@ -100,7 +76,7 @@ hipError_t gemv_bias_silu_bf16(const bf16* a, int lda, const bf16* W, int ldw, c
 // row, unused}.  q, k: [heads][rp][64], vt: [heads][64][rp].  chunk == 0: full attention
 // inside each document; chunk > 0: key visible iff (key_pos / chunk) <= (query_pos / chunk).
 // n_tiles is the grid's capacity; tiles_live (when not null) holds the live tile count.
-hipError_t attention_varlen(const bf16* q, const bf16* k, const bf16* vt, bf16* o,
+hipError_t attention_varlen(const f16* q, const f16* k, const f16* vt, f16* o,
                             const int32_t* tiles, int n_tiles, int rp, int heads, int chunk,
                             hipStream_t stream, const int32_t* tiles_live = nullptr);
 constexpr int kAttnTileInts = 4;  // ints per tile entry
@@ -108,15 +84,15 @@ constexpr int kAttnTileQ = 128;
 
 // ---- causal grouped conv position embedding (64 channels per group) -------------------------
 // y[r, g*64+co] = mish(bias + sum_{j,ci} W[g][j][co][ci] x[r-(taps-1)+j, g*64+ci]), rows before
-// the row's document start read as zero.  out_bf16 != null: store y;  h != null: h += y.
-hipError_t conv_causal_mish(const bf16* x, int C, const bf16* w, const float* bias, int taps,
-                            const int32_t* pos, int rows, bf16* out_bf16, float* h,
+// the row's document start read as zero.  out_f16 != null: store y;  h != null: h += y.
+hipError_t conv_causal_mish(const f16* x, int C, const f16* w, const float* bias, int taps,
+                            const int32_t* pos, int rows, f16* out_f16, float* h,
                             hipStream_t stream, const int32_t* rows_live = nullptr);
 
 // ---- bandwidth-bound kernels -----------------------------------------------------------------
-// out[r, :] = bf16(LN(h[r, :]) * scale + shift), scale/shift rows = mod + docid[r]*mod_stride + off
+// out[r, :] = f16(LN(h[r, :]) * scale + shift), scale/shift rows = mod + docid[r]*mod_stride + off
 hipError_t layer_norm_modulate(const float* h, int C, int rows, const float* mod, long mod_stride,
-                               int shift_off, int scale_off, const int32_t* docid, bf16* out,
+                               int shift_off, int scale_off, const int32_t* docid, f16* out,
                                hipStream_t stream, const int32_t* rows_live = nullptr);
 
 // docid[r], pos[r] from device cu_seqlens[n_docs+1].
@@ -130,13 +106,13 @@ hipError_t build_aligned_row_index(const int32_t* cu_int, const int32_t* lens,
                                    const int32_t* cu_ext, int n_docs, int rows_int, int32_t* docid,
                                    int32_t* pos, int32_t* ext_row, hipStream_t stream);
 
-// a[r, 0:4*mel] = bf16([x[e], cond[e], mu[e], spks[docid[r]]]) with e = ext_row[r]; zeros when e < 0
+// a[r, 0:4*mel] = f16([x[e], cond[e], mu[e], spks[docid[r]]]) with e = ext_row[r]; zeros when e < 0
 hipError_t pack_inputs(const float* x, const float* cond, const float* mu, const float* spks,
-                       const int32_t* docid, const int32_t* ext_row, int rows, int mel, bf16* a,
+                       const int32_t* docid, const int32_t* ext_row, int rows, int mel, f16* a,
                        hipStream_t stream, const int32_t* rows_live = nullptr);
 
-// out[m, 0:dim] = bf16([sin(1000 t_m f), cos(1000 t_m f)]), f_i = exp(-i ln(1e4)/(dim/2-1))
-hipError_t timestep_sinusoid(const float* t, int n_t, int dim, bf16* out, hipStream_t stream);
+// out[m, 0:dim] = f16([sin(1000 t_m f), cos(1000 t_m f)]), f_i = exp(-i ln(1e4)/(dim/2-1))
+hipError_t timestep_sinusoid(const float* t, int n_t, int dim, f16* out, hipStream_t stream);
 
 // x[r] += dt * ((1+cfg) v[r] - cfg v[r+rc]); x[r+rc] = x[r]   for r < rc
 // (rc = rc_live[0] when rc_live is not null; the grid covers the capacity rc)

@@ -243,7 +243,8 @@ class DiTEstimator(nn.Module, _PackedRunner):
 
     @torch.no_grad()
     def finalize_weights(self) -> None:
-        """Derive the kernel-layout bf16 weights once (flashinfer_dit.py:228-313).
+        """Derive the kernel-layout fp16 weights once (flashinfer_dit.py:228-313); fp16 is the
+        dtype the reference's apply_flashinfer gives the DiT (flashinfer_dit.py:963).
 
         Fused QKV per block; "+1" folded into the AdaLN scale biases (chunks 1 and 4 of every
         block, chunk 0 of the final (scale, shift) pair); all AdaLN projections concatenated
@@ -256,7 +257,7 @@ class DiTEstimator(nn.Module, _PackedRunner):
             raise ValueError("DiTEstimator runs on a GPU device")
         lib = _lib.load()
         dev, D, L = self.device, self.dim, self.depth
-        bf = lambda t: t.detach().to(device=dev, dtype=torch.bfloat16).contiguous()
+        bf = lambda t: t.detach().to(device=dev, dtype=torch.float16).contiguous()
         f32 = lambda t: t.detach().to(device=dev, dtype=torch.float32).contiguous()
         blocks = self.transformer_blocks
 

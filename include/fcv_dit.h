@@ -48,21 +48,22 @@ typedef struct FcvDitDims {
 } FcvDitDims;
 
 /* Derived inference weights (device pointers, caller-owned, must outlive the handle).
- * bf16 tensors are raw 16-bit words.  Derivation follows FlashInferDiT.finalize_weights
+ * Weight matrices are IEEE fp16 (the dtype apply_flashinfer gives the reference's DiT,
+ * flashinfer_dit.py:963), biases and RoPE tables fp32.  Derivation follows FlashInferDiT.finalize_weights
  * (flashinfer_dit.py:228-313): fused QKV, "+1" folded into the AdaLN scale biases, one
  * concatenated AdaLN projection, conv weights re-laid out per group and tap. */
 typedef struct FcvDitWeights {
-  const void* temb_w1;  const float* temb_b1;  /* bf16 [dim][256], fp32 [dim] */
-  const void* temb_w2;  const float* temb_b2;  /* bf16 [dim][dim] */
-  const void* ada_w;    const float* ada_b;    /* bf16 [depth*6*dim + 2*dim][dim] */
-  const void* in_w;     const float* in_b;     /* bf16 [dim][4*mel] (x, cond, mu, spks) */
-  const void* conv1_w;  const float* conv1_b;  /* bf16 [groups][kernel][64][64] (g, tap, co, ci) */
+  const void* temb_w1;  const float* temb_b1;  /* fp16 [dim][256], fp32 [dim] */
+  const void* temb_w2;  const float* temb_b2;  /* fp16 [dim][dim] */
+  const void* ada_w;    const float* ada_b;    /* fp16 [depth*6*dim + 2*dim][dim] */
+  const void* in_w;     const float* in_b;     /* fp16 [dim][4*mel] (x, cond, mu, spks) */
+  const void* conv1_w;  const float* conv1_b;  /* fp16 [groups][kernel][64][64] (g, tap, co, ci) */
   const void* conv2_w;  const float* conv2_b;
-  const void* qkv_w;    const float* qkv_b;    /* bf16 [depth][3*dim][dim] */
-  const void* out_w;    const float* out_b;    /* bf16 [depth][dim][dim] */
-  const void* ff1_w;    const float* ff1_b;    /* bf16 [depth][ff][dim] */
-  const void* ff2_w;    const float* ff2_b;    /* bf16 [depth][dim][ff] */
-  const void* proj_w;   const float* proj_b;   /* bf16 [128][dim], fp32 [128]; rows >= mel zero */
+  const void* qkv_w;    const float* qkv_b;    /* fp16 [depth][3*dim][dim] */
+  const void* out_w;    const float* out_b;    /* fp16 [depth][dim][dim] */
+  const void* ff1_w;    const float* ff1_b;    /* fp16 [depth][ff][dim] */
+  const void* ff2_w;    const float* ff2_b;    /* fp16 [depth][dim][ff] */
+  const void* proj_w;   const float* proj_b;   /* fp16 [128][dim], fp32 [128]; rows >= mel zero */
   const float* rope_cos; const float* rope_sin; /* fp32 [max_pos][rope_dim/2] */
 } FcvDitWeights;
 
@@ -135,7 +136,7 @@ int fcv_dit_solve(FcvDit* dit, float* x, const float* mu, const float* cond, con
 
 /* A solve schedule shared by handles: the modulation rows of an n_steps Euler schedule (every
  * block's AdaLN shift/scale/gate and the final (scale, shift), _project_modulations
- * flashinfer_dit.py:430-445, plus the LayerNorm fold's column terms) for t_host[0..n_steps),
+ * flashinfer_dit.py:430-445) for t_host[0..n_steps),
  * computed once by fcv_dit_schedule into a caller buffer of fcv_dit_schedule_bytes(dit,
  * n_steps) bytes (256-byte aligned; 0 for an invalid n_steps).  fcv_dit_solve_scheduled is
  * fcv_dit_solve reading its modulation rows from that buffer instead of computing them: the
@@ -173,8 +174,8 @@ int fcv_dit_plan_info(const FcvDit* dit, int32_t* rows, int32_t* n_docs, int32_t
  * plan_calls counter, flashinfer_attention.py:61-62); it lets a benchmark time one kernel live
  * inside a solve.  Arms a probe on `stage`: during every later forward/solve call the library
  * records a HIP event pair (timing-only events, no system-scope fence) around that stage's
- * launch in block 1 (the first block whose LayerNorms fold into its GEMMs, whose launches every
- * later block repeats; block 0 for a one-block model and for the LN-modulate stage), or around
+ * launch in block 1 (whose launches every later block repeats; block 0 for a one-block
+ * model), or around
  * its one launch for stages outside the blocks, for the first n_pairs launches counted from the
  * start of the call.  With repeat > 1 the probed launch is issued
  * `repeat` times back to back between the two events, so per-launch event overhead is

@@ -19,9 +19,9 @@ def say(*args) -> None:
     sys.stdout.flush()
 
 
-def bf16_weights(sd: dict) -> dict:
-    """The oracle's view of the weights the GPU path stores in bf16 (biases stay fp32)."""
-    return {k: (v.to(torch.bfloat16).float() if k.endswith("weight") else v) for k, v in sd.items()}
+def f16_weights(sd: dict) -> dict:
+    """The oracle's view of the weights the GPU path stores in fp16 (biases stay fp32)."""
+    return {k: (v.to(torch.float16).float() if k.endswith("weight") else v) for k, v in sd.items()}
 
 
 def make_estimator(fcv, sd: dict, depth: int, **kw):

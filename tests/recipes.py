@@ -2,11 +2,13 @@
 
 With the plain N(0, 0.02) weights the attention logits have a deviation of about 0.4, the
 softmax is nearly uniform, and dropping RoPE moves a 22-block velocity by only ~1e-3, below
-the 1e-2 parity bar.  The recipes below draw ``to_q`` / ``to_k`` with a deviation of 0.05-0.06
-(logit deviation ~2.6-3.7) and push the AdaLN gates up, so every block's attention matters.
-Sharper attention also amplifies the bf16 rounding of q and k: at 0.06 the 22-block model's
-GPU error reaches the 1e-2 bar itself (1.19e-2 measured), at 0.05 it is ~6e-3 while every
-mutant below still moves the velocity by more than 5x the bar.
+the 1e-2 parity bar.  The recipes below draw ``to_q`` / ``to_k`` with a deviation of 0.06
+(logit deviation ~3.7) and push the AdaLN gates up, so every block's attention matters.
+Sharper attention amplifies every rounding of the forward: on the 22-block recipe a CPU
+emulation of the kernels' roundings puts the velocity error at 9.9e-3 (full) and 1.16e-2
+(chunk-causal) with bf16 weights and operands, and at 1.2e-3 / 1.5e-3 with fp16 weights and
+operands (the reference's dtype, flashinfer_dit.py:963), which the kernels use, so the
+peaked tests hold the GPU to ``PEAKED_TOL``, half the parity bar.
 ``tests/test_oracle_power.py`` proves on the CPU, with these exact weights and inputs, that
 removing RoPE, reversing it, flattening the softmax or moving the chunk boundary by one frame
 moves the oracle's velocity by at least 5x the tolerance the GPU tests hold the kernels to.
@@ -17,9 +19,10 @@ from __future__ import annotations
 import torch
 
 VEL_TOL = 1e-2  # per-step velocity rel-L2 against the fp32 oracle (the parity bar)
+PEAKED_TOL = 5e-3  # the peaked-attention recipes' bar: half the parity bar
 
 # 22 blocks; the CFG pair of one 550-frame request (prompt 250), t = 0.5
-SHARP22 = dict(depth=22, seed=41, qk_std=0.05, gate_bias=0.2)
+SHARP22 = dict(depth=22, seed=41, qk_std=0.06, gate_bias=0.2)
 # 2 blocks; one document as long as the RoPE tables between short documents
 SHARP2 = dict(depth=2, seed=43, qk_std=0.06, gate_bias=0.5)
 MAX_POS = 4096

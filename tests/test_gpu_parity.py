@@ -1,7 +1,7 @@
 """GPU parity of the HIP estimator against the fp32 CPU oracle and the reference golden vectors.
 
 Tolerances: per-step velocity rel-L2 <= 1e-2 vs the fp32 path, mel rel-L2 <= 2e-2 after 10
-Euler steps.  Where the oracle is given the same bf16-rounded
+Euler steps.  Where the oracle is given the same fp16-rounded
 weights the GPU uses, the remaining error is activation rounding only and the bound is tighter.
 """
 
@@ -16,14 +16,14 @@ import torch
 
 from oracle import dit_oracle as O
 from tests import recipes
-from tests.gpu_helpers import (bf16_weights, make_estimator, oracle_packed, random_packed, rel_l2,
+from tests.gpu_helpers import (f16_weights, make_estimator, oracle_packed, random_packed, rel_l2,
                                say)
 
 pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 VEL_TOL = 1e-2        # per-step velocity vs the fp32 reference path
-BF16_W_TOL = 5e-3     # vs the oracle running on the same bf16-rounded weights
+F16_W_TOL = 5e-3      # vs the oracle running on the same fp16-rounded weights
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -50,10 +50,10 @@ def test_one_block_300_frames(fcv, streaming):
     say(f"[one_block] streaming={streaming}")
     v = est.forward_packed(x, mu, cond, spks, t, [300], streaming=streaming).cpu()
     ref32 = oracle_packed(sd, x, mu, cond, spks, t, [300], streaming)
-    ref16 = oracle_packed(bf16_weights(sd), x, mu, cond, spks, t, [300], streaming)
+    ref16 = oracle_packed(f16_weights(sd), x, mu, cond, spks, t, [300], streaming)
     e32, e16 = rel_l2(v, ref32), rel_l2(v, ref16)
-    say(f"[one_block] rel_l2 vs fp32 {e32:.2e}, vs bf16-weight oracle {e16:.2e}")
-    assert e32 <= VEL_TOL and e16 <= BF16_W_TOL
+    say(f"[one_block] rel_l2 vs fp32 {e32:.2e}, vs fp16-weight oracle {e16:.2e}")
+    assert e32 <= VEL_TOL and e16 <= F16_W_TOL
 
 
 @pytest.mark.parametrize("streaming", [False, True])
@@ -77,20 +77,20 @@ def test_reference_golden_block(fcv, streaming):
 @pytest.mark.parametrize("streaming", [False, True])
 def test_ragged_docs_two_blocks(fcv, stress2, streaming, shared_t):
     """Ragged packing edge cases: a 1-frame doc, a doc of exactly one 128-row tile, docs that
-    straddle tiles, chunk boundaries not aligned to tiles.  With one t per document every
-    LayerNorm is a pass of its own; with one shared t they fold into the GEMMs."""
+    straddle tiles, chunk boundaries not aligned to tiles; one t per document and one shared
+    t."""
     sd, est = stress2
     lengths = [37, 128, 1, 200, 75]
     x, mu, cond, spks, t = random_packed(lengths, seed=2)
     if shared_t:
         t = t[:1]
     v = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming).cpu()
-    ref = oracle_packed(bf16_weights(sd), x, mu, cond, spks, t, lengths, streaming)
+    ref = oracle_packed(f16_weights(sd), x, mu, cond, spks, t, lengths, streaming)
     off = 0
     for n in lengths:
         e = rel_l2(v[off:off + n], ref[off:off + n])
         say(f"[ragged] streaming={streaming} shared_t={shared_t} len={n} rel_l2 {e:.2e}")
-        assert e <= BF16_W_TOL
+        assert e <= F16_W_TOL
         off += n
 
 
@@ -104,10 +104,10 @@ def test_long_document(fcv, stress2, streaming):
     say(f"[long_doc] streaming={streaming} GPU forward")
     v = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming).cpu()
     say(f"[long_doc] streaming={streaming} oracle forward")
-    ref = oracle_packed(bf16_weights(sd), x, mu, cond, spks, t, lengths, streaming)
+    ref = oracle_packed(f16_weights(sd), x, mu, cond, spks, t, lengths, streaming)
     e_long, e_short = rel_l2(v[:2500], ref[:2500]), rel_l2(v[2500:], ref[2500:])
     say(f"[long_doc] streaming={streaming} rel_l2 long {e_long:.2e} short {e_short:.2e}")
-    assert e_long <= BF16_W_TOL and e_short <= BF16_W_TOL
+    assert e_long <= F16_W_TOL and e_short <= F16_W_TOL
 
 
 @pytest.mark.parametrize("streaming", [False, True])
@@ -122,16 +122,16 @@ def test_max_pos_document_among_many_tiny_ones(fcv, stress2, streaming):
     tiny = torch.randint(1, 41, (150,), generator=g).tolist()
     lengths = tiny[:75] + [est.max_pos] + tiny[75:]
     x, mu, cond, spks, t = random_packed(lengths, seed=19)
-    t = t[:1]  # one t for every document, as in a solver step: the folded LayerNorms
+    t = t[:1]  # one t for every document, as in a solver step
     say(f"[limits] streaming={streaming} {len(lengths)} docs, {sum(lengths)} rows, GPU forward")
     v = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming).cpu()
     say(f"[limits] streaming={streaming} oracle forward")
-    ref = oracle_packed(bf16_weights(sd), x, mu, cond, spks, t, lengths, streaming)
+    ref = oracle_packed(f16_weights(sd), x, mu, cond, spks, t, lengths, streaming)
     off, worst = 0, 0.0
     for n in lengths:
         e = rel_l2(v[off:off + n], ref[off:off + n])
         worst = max(worst, e)
-        assert e <= BF16_W_TOL, f"document of {n} rows at row {off}: rel_l2 {e:.2e}"
+        assert e <= F16_W_TOL, f"document of {n} rows at row {off}: rel_l2 {e:.2e}"
         off += n
     say(f"[limits] streaming={streaming} worst per-document rel_l2 {worst:.2e}")
 
@@ -158,16 +158,13 @@ def test_concurrent_request_groups_equal_one_batch(fcv, stress2):
 
 
 def test_shared_t_equals_per_doc_t(fcv, stress2):
-    """One shared t against the same t repeated per document, for 2, 16 and 20 documents.  With
-    one t for every document the LayerNorms fold into the GEMMs (statistics and bf16(h * scale)
-    from the gated-residual epilogues); with one t per document each LayerNorm is a pass of its
-    own that writes the normalized bf16 rows.  The two paths round differently, so they agree
-    to bf16 accuracy, not bit for bit.  Per-document t values are then checked bit for bit
-    against themselves: reversing the documents (and their t) moves documents between the
-    first and the second launch of the 16-row skinny product that computes the modulation rows,
-    and every document's rows stay identical, so the rows past the first launch are indexed
-    right.  Each document alone at its own t (one t: the folded path) agrees with its rows of
-    the per-document call to the same bf16 accuracy."""
+    """One shared t against the same t repeated per document, for 2, 16 and 20 documents, bit
+    for bit: a document's modulation row is the same whichever way it is computed, and the
+    LayerNorm passes and gated residuals apply it the same way.  Per-document t values are then
+    checked against themselves: reversing the documents (and their t) moves documents between
+    the first and the second launch of the 16-row skinny product that computes the modulation
+    rows, and every document's rows stay identical, so the rows past the first launch are
+    indexed right; each document alone at its own t equals its rows of the per-document call."""
     sd, est = stress2
     g = torch.Generator().manual_seed(3)
     for n_docs in (2, 16, 20):
@@ -176,7 +173,7 @@ def test_shared_t_equals_per_doc_t(fcv, stress2):
         say(f"[shared_t] {n_docs} documents")
         a = est.forward_packed(x, mu, cond, spks, torch.tensor([0.3]), lengths)
         b = est.forward_packed(x, mu, cond, spks, torch.full((n_docs,), 0.3), lengths)
-        assert rel_l2(a, b) < BF16_W_TOL, n_docs
+        assert torch.equal(a, b), n_docs
     t = torch.rand(n_docs, generator=g)
     full = est.forward_packed(x, mu, cond, spks, t, lengths)
     cu = [0]
@@ -190,33 +187,36 @@ def test_shared_t_equals_per_doc_t(fcv, stress2):
     for d, n in enumerate(lengths):
         alone = est.forward_packed(x[cu[d]:cu[d + 1]], mu[cu[d]:cu[d + 1]], cond[cu[d]:cu[d + 1]],
                                    spks[d:d + 1], t[d:d + 1], [n])
-        assert rel_l2(alone, full[cu[d]:cu[d + 1]]) < BF16_W_TOL, d
+        assert torch.equal(alone, full[cu[d]:cu[d + 1]]), d
 
 
-def test_folded_layernorm_with_offset_residual(fcv):
-    """The folded LayerNorm rounds bf16(h * scale) instead of the normalized row, so its error
-    grows with the row mean relative to the spread.  With +3 on every input-projection bias
-    (the residual stream then carries a large mean) the folded path (one shared t) stays within
-    the velocity bound of the fp32 oracle; a bf16 emulation of both paths on the CPU puts it at
-    4.5e-3 against the bf16-weight oracle where the LN-pass path (the same t per document) is
-    at 3.5e-3 (3.0e-3 both without the offset).  The LN-pass path keeps the bf16-weight
-    bound."""
+def test_layernorm_with_large_residual_mean(fcv):
+    """A residual stream whose row mean is at least 20 times its spread (+20 on every bias of
+    the second position-embedding conv: Mish of a large argument is that argument, so every
+    row of the residual gains ~20 while its spread stays ~0.4; the ratio is measured on the
+    oracle's input embedding below).  Each
+    LayerNorm takes its statistics in fp32 from the fp32 residual and writes the normalized,
+    modulated fp16 row, the tensor the reference itself materializes, so the mean costs no
+    precision: the forward keeps the velocity bar against the fp32 oracle and the tighter bar
+    against the fp16-weight oracle."""
     dims = fcv.synthetic.DiTDims(depth=2)
     sd = fcv.synthetic.random_state_dict(dims, seed=21, gate_bias=0.5)
-    sd["input_embed.proj.bias"] = sd["input_embed.proj.bias"] + 3.0
+    key = "input_embed.conv_pos_embed.conv2.0.bias"
+    sd[key] = sd[key] + 20.0
     est = make_estimator(fcv, sd, depth=2)
     lengths = [200, 75, 31]
     x, mu, cond, spks, t = random_packed(lengths, seed=29)
     t = t[:1]
+    h = O.input_embedding(sd, x[None, :200], cond[None, :200], mu[None, :200], spks[:1])[0]
+    ratio = float((h.mean(-1).abs() / h.std(-1)).min())
+    say(f"[large_mean] residual |mean| / spread after the input embedding: min {ratio:.1f}")
+    assert ratio >= 20.0
     ref32 = oracle_packed(sd, x, mu, cond, spks, t, lengths)
-    ref16 = oracle_packed(bf16_weights(sd), x, mu, cond, spks, t, lengths)
-    folded = est.forward_packed(x, mu, cond, spks, t, lengths).cpu()
-    ln_pass = est.forward_packed(x, mu, cond, spks, t.expand(len(lengths)).clone(), lengths).cpu()
-    say(f"[offset_residual] vs fp32 oracle: folded {rel_l2(folded, ref32):.2e}, LN pass "
-        f"{rel_l2(ln_pass, ref32):.2e}; vs bf16-weight oracle: folded {rel_l2(folded, ref16):.2e}, "
-        f"LN pass {rel_l2(ln_pass, ref16):.2e}")
-    assert rel_l2(folded, ref32) <= VEL_TOL
-    assert rel_l2(ln_pass, ref16) <= BF16_W_TOL
+    ref16 = oracle_packed(f16_weights(sd), x, mu, cond, spks, t, lengths)
+    v = est.forward_packed(x, mu, cond, spks, t, lengths).cpu()
+    e32, e16 = rel_l2(v, ref32), rel_l2(v, ref16)
+    say(f"[large_mean] rel_l2 vs fp32 oracle {e32:.2e}, vs fp16-weight oracle {e16:.2e}")
+    assert e32 <= VEL_TOL and e16 <= F16_W_TOL
 
 
 def test_padded_dropin_collapses_equal_t(fcv, stress2):
@@ -240,10 +240,11 @@ def test_padded_dropin_collapses_equal_t(fcv, stress2):
 
 
 def test_solve_twenty_steps_equals_stepwise(fcv, stress2):
-    """A 20-step solve computes the modulation rows of steps 0-15 in one pass and of steps
-    16-19 in a second one.  Eager, on its first capture and on a replay, it gives bit for bit
-    the sample of 20 single forwards (each with its own shared t) each followed by the CFG
-    Euler update of the C ABI, with the same cosine schedule."""
+    """A 20-step solve reads the estimator's 20-step schedule, whose modulation rows come from
+    two passes of the skinny product (steps 0-15, then 16-19).  Eager, on its first capture and
+    on a replay, it gives bit for bit the sample of 20 single forwards (each computing its own
+    shared-t modulation row) each followed by the CFG Euler update of the C ABI, with the same
+    cosine schedule."""
     _, est = stress2
     b = fcv.synthetic.make_batch("steps20", [70, 33, 41], [20, 10, 15], seed=61)
     ts, dts = fcv.euler_schedule(20)
@@ -266,22 +267,46 @@ def test_solve_twenty_steps_equals_stepwise(fcv, stress2):
         assert torch.equal(got, want), graph
 
 
+def _solve_unscheduled(fcv, est, b, n_steps):
+    """The sample of fcv_dit_solve, the C ABI's solve that computes its own modulation rows in
+    the loop (kModGroup steps per pass), eager, on an exact plan of the CFG layout."""
+    lib = fcv._lib.load()
+    dev = "cuda:0"
+    inp = b.cfg_inputs()
+    est.plan(b.doc_lengths)
+    x, mu, cond, spks = (inp[k].to(dev).contiguous() for k in ("x", "mu", "cond", "spks"))
+    ts, dts = fcv.euler_schedule(n_steps)
+    t_arr = (fcv._lib.c_float * n_steps)(*ts)
+    dt_arr = (fcv._lib.c_float * n_steps)(*dts)
+    fcv._lib.check(lib.fcv_dit_solve(est._require(), x.data_ptr(), mu.data_ptr(),
+                                     cond.data_ptr(), spks.data_ptr(), t_arr, dt_arr, n_steps,
+                                     0.7, 0, est._stream_ptr()))
+    torch.cuda.synchronize()
+    return x[:sum(b.lengths)].cpu()
+
+
 def test_shared_schedule_twenty_steps(fcv, stress2):
-    """The solve schedule shared by request groups (fcv_dit_schedule, then
-    fcv_dit_solve_scheduled on each group's handle): 20 steps, so the schedule holds rows past
-    one 16-row pass of the skinny product.  Two and three groups give bit for bit the sample of
-    one group solving with its own modulation rows (fcv_dit_solve), eagerly, on the first
-    capture and on a replay; a schedule buffer too small for the step count is refused."""
+    """The solve schedule (fcv_dit_schedule, then fcv_dit_solve_scheduled on each group's
+    handle): 20 steps, so the schedule holds rows past one 16-row pass of the skinny product.
+    It is computed once per estimator and step count and reused by every later solve.  One,
+    two and three groups give bit for bit the sample of fcv_dit_solve, which computes its own
+    modulation rows, eagerly, on the first capture and on a replay; a schedule buffer too
+    small for the step count is refused."""
     _, est = stress2
     b = fcv.synthetic.make_batch("sched20", [70, 33, 41, 90], [20, 10, 15, 30], seed=62)
     solve = lambda c, graph: fcv.solve_euler_packed(
         est, b.noise, b.mu, b.cond, b.spks, b.lengths, n_steps=20, use_graph=graph,
         concurrency=c).cpu()
-    ref = solve(1, False)
-    for c in (2, 3):
+    say("[sched20] fcv_dit_solve (modulation rows computed in the loop)")
+    ref = _solve_unscheduled(fcv, est, b, 20)
+    first = None
+    for c in (1, 2, 3):
         for graph in (False, True, True):
             say(f"[sched20] groups={c} graph={graph}")
             assert torch.equal(solve(c, graph), ref), (c, graph)
+            buf, _ = est._schedules[20]
+            first = first or buf.data_ptr()
+            assert buf.data_ptr() == first  # one schedule, computed by the first solve
     lib = fcv._lib.load()
     handle = est._require()
     small = lib.fcv_dit_schedule_bytes(handle, 10)
@@ -297,7 +322,7 @@ def test_shared_schedule_twenty_steps(fcv, stress2):
 
 @pytest.mark.parametrize("streaming", [False, True])
 def test_peaked_attention_depth22(fcv, sharp22, streaming):
-    """22 blocks on the peaked-attention recipe (q/k weights of deviation 0.05, gates +0.2):
+    """22 blocks on the peaked-attention recipe (q/k weights of deviation 0.06, gates +0.2):
     the 550-frame CFG pair against the fp32 oracle.  On these weights and inputs dropping or
     reversing RoPE, a uniform softmax or a chunk boundary one frame off moves the oracle
     velocity by 5-50x the tolerance (tests/test_oracle_power.py), so this bar pins the RoPE
@@ -310,7 +335,7 @@ def test_peaked_attention_depth22(fcv, sharp22, streaming):
     ref = oracle_packed(sd, x, mu, cond, spks, t, lengths, streaming)
     err = rel_l2(v, ref)
     say(f"[peaked22] streaming={streaming} velocity rel_l2 vs fp32 oracle {err:.2e}")
-    assert err <= recipes.VEL_TOL
+    assert err <= recipes.PEAKED_TOL
 
 
 @pytest.mark.parametrize("streaming", [False, True])
@@ -331,7 +356,7 @@ def test_peaked_attention_max_pos_document(fcv, streaming):
     rest[long] = False
     e_long, e_rest = rel_l2(v[long], ref[long]), rel_l2(v[rest], ref[rest])
     say(f"[peaked_max_pos] streaming={streaming} rel_l2 long {e_long:.2e} short docs {e_rest:.2e}")
-    assert e_long <= recipes.VEL_TOL and e_rest <= recipes.VEL_TOL
+    assert e_long <= recipes.PEAKED_TOL and e_rest <= recipes.PEAKED_TOL
 
 
 def test_padded_dropin_matches_packed(fcv, stress2):
@@ -435,7 +460,7 @@ def test_every_gemm_tile_shape_gives_the_same_bits(fcv, stress2, monkeypatch):
     """The GEMM tile shape only decides which rows and columns share a workgroup, never an
     element's K order.  Forcing each of the eight shapes (FCV_GEMM_TILE, wherever it divides
     the output width) reproduces the default choice bit for bit, with the full and the
-    chunk-causal mask and with one shared t (the folded LayerNorm) and one t per document."""
+    chunk-causal mask and with one shared t and one t per document."""
     sd, est = stress2
     lengths = [90, 300, 17, 150]
     x, mu, cond, spks, t_doc = random_packed(lengths, seed=8)

@@ -21,6 +21,7 @@ import pytest
 import torch
 
 from oracle import dit_oracle as O
+from tests import recipes
 from tests.gpu_helpers import oracle_packed, rel_l2, say
 
 pytestmark = pytest.mark.gpu
@@ -132,3 +133,23 @@ def test_headline_workload_against_oracle(fcv, full22):
     say(f"[headline] worst step velocity {max(errs):.2e}, Mel after 10 steps {err:.2e}")
     assert len(errs) == b.n_steps and max(errs) <= VEL_TOL
     assert err <= 2e-2
+
+
+def test_headline_workload_peaked_attention(fcv, sharp22):
+    """Workload 3's 16 documents (123-1291 frames) through one forward of the 22-block
+    peaked-attention recipe (tests/recipes.py) at t = 0.5, against the fp32 oracle over all
+    9184 rows.  The plain weights of the headline test leave the softmax nearly uniform; on
+    these, RoPE, the softmax and the document mask move the velocity by many times the bar
+    (tests/test_oracle_power.py), so this pins them at the benchmark's own document lengths."""
+    sd, est = sharp22
+    b = fcv.synthetic.workload(3)
+    inp = b.cfg_inputs()
+    t = torch.tensor([0.5])
+    say(f"[headline_peaked] GPU forward, {len(b.doc_lengths)} docs, {b.rows} rows")
+    v = est.forward_packed(inp["x"], inp["mu"], inp["cond"], inp["spks"], t,
+                           b.doc_lengths).cpu()
+    say("[headline_peaked] oracle forward")
+    ref = oracle_packed(sd, inp["x"], inp["mu"], inp["cond"], inp["spks"], t, b.doc_lengths)
+    err = rel_l2(v, ref)
+    say(f"[headline_peaked] velocity rel_l2 over 16 docs vs fp32 oracle {err:.2e}")
+    assert err <= recipes.PEAKED_TOL
