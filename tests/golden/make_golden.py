@@ -25,6 +25,13 @@ are not fixed by any closed form.  The generator is built at a reduced width (ba
 stages) from its own source; our seeded weights are loaded into it with ``strict=True`` (which
 also pins the ``hift.pt`` parameter names), and its fixed random buffers are stored with the
 outputs.  ``--only hift`` writes just that file.
+
+``prelookahead.npz`` pins the front-end oracle's ``pre_lookahead`` to the reference's own
+``PreLookaheadLayer`` (cosyvoice/transformer/upsample_encoder.py:55-92) at the flow's shape
+(builders.py:32-34: 80 -> 1024 -> 80, lookahead 3), with our seeded flow weights loaded
+``strict=True``: a finalized padded batch of two sequences (zero right pad, one shorter than
+the other) and the streaming form with a 3-frame right context (``flashinfer_flow.py:198-204``).
+``--only frontend`` writes just that file.
 """
 
 from __future__ import annotations
@@ -161,16 +168,47 @@ def hift_golden() -> None:
         rand_ini=gen.rand_ini.numpy(), sine_waves=gen.sine_waves[:, :L].numpy(), **out)
 
 
+def frontend_golden() -> None:
+    """The reference's PreLookaheadLayer at the flow's shape, finalized and with context."""
+    from faster_cosyvoice.token2wav.cosyvoice.transformer.upsample_encoder import (  # noqa: E402
+        PreLookaheadLayer)
+
+    syn = _synthetic()
+    torch.set_grad_enabled(False)
+    dims = syn.FlowDims()
+    sd = syn.random_flow_state_dict(dims, seed=71)
+    layer = PreLookaheadLayer(in_channels=dims.feat, channels=dims.channels,
+                              pre_lookahead_len=dims.lookahead)
+    prefix = "pre_lookahead_layer."
+    layer.load_state_dict({k[len(prefix):]: v for k, v in sd.items() if k.startswith(prefix)},
+                          strict=True)
+    layer.eval()
+    rng = np.random.Generator(np.random.PCG64(72))
+    x = rng.standard_normal((2, 13, dims.feat)).astype(np.float32)
+    x[1, 9:] = 0.0  # the second sequence is 9 frames long, zero-padded as the flow's mask leaves it
+    out_final = layer(torch.from_numpy(x))
+    xs = rng.standard_normal((1, 10, dims.feat)).astype(np.float32)
+    ctx = rng.standard_normal((1, dims.lookahead, dims.feat)).astype(np.float32)
+    out_ctx = layer(torch.from_numpy(xs), torch.from_numpy(ctx))
+    np.savez_compressed(HERE / "prelookahead.npz", weight_seed=np.int32(71),
+                        lookahead=np.int32(dims.lookahead), x=x, out_final=out_final.numpy(),
+                        x_stream=xs, context=ctx, out_context=out_ctx.numpy())
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", default="/root/reference")
-    ap.add_argument("--only", choices=["hift"], default=None)
+    ap.add_argument("--only", choices=["hift", "frontend"], default=None)
     args = ap.parse_args()
     _install_stubs()
     sys.path.insert(0, args.ref)
     if args.only == "hift":
         hift_golden()
         print("wrote hift_small.npz")
+        return
+    if args.only == "frontend":
+        frontend_golden()
+        print("wrote prelookahead.npz")
         return
     from faster_cosyvoice.token2wav.cosyvoice.flow.DiT.dit import DiT  # noqa: E402
     from faster_cosyvoice.token2wav.flashinfer_flow import solve_euler_batched  # noqa: E402
@@ -222,6 +260,7 @@ def main() -> None:
         weight_seed=np.int32(5), gate_bias=np.float32(0.5), dim=np.int32(1024), depth=np.int32(1),
         heads=np.int32(16), out_full=out_full.numpy(), out_stream=out_stream.numpy())
     hift_golden()
+    frontend_golden()
     print("wrote", sorted(p.name for p in HERE.glob("*.npz")))
 
 

@@ -1,7 +1,10 @@
-"""CPU checks that pin the Flow front-end oracle (oracle/frontend_oracle.py) by closed forms and
-invariants; no reference code runs for it.
+"""CPU checks that pin the Flow front-end oracle (oracle/frontend_oracle.py) by closed forms,
+invariants and the reference's own layer.
 
-``PreLookaheadLayer`` (upsample_encoder.py:55-92) is pinned piece by piece: the direction and
+``tests/golden/prelookahead.npz`` holds the outputs of the reference's ``PreLookaheadLayer``
+(upsample_encoder.py:55-92, written by tests/golden/make_golden.py at the flow's shape with our
+seeded weights): a finalized padded batch and the streaming form with a right context.
+Beyond that, ``PreLookaheadLayer`` (upsample_encoder.py:55-92) is pinned piece by piece: the direction and
 tap order of the lookahead convolution and the LeakyReLU slope (a one-tap identity conv1 gives
 leaky_relu(x[t+2])), the causal left padding of conv2 (its last tap is the current frame; the
 receptive field of output t is exactly t-2 .. t+3), the residual (zero conv2 gives x + b2), the
@@ -14,9 +17,14 @@ forms.
 
 from __future__ import annotations
 
+from pathlib import Path
+
+import numpy as np
 import torch
 
 from oracle import frontend_oracle as F
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
 def _weights(C=64, seed=3):
@@ -154,3 +162,21 @@ def test_streaming_features_with_context(fcv):
     full = F.streaming_token_features(sd, toks, finalize=True)
     assert out.shape == (1, 20, 80) and full.shape == (1, 26, 80)
     torch.testing.assert_close(out, full[:, :20], rtol=1e-5, atol=1e-5)
+
+
+def test_pre_lookahead_matches_reference_golden(fcv):
+    """The oracle's pre_lookahead against the reference's PreLookaheadLayer on the same seeded
+    weights (tests/golden/prelookahead.npz): the finalized padded batch (zero right pad) and a
+    non-final stream whose last 3 frames arrive as right context."""
+    g = dict(np.load(GOLDEN / "prelookahead.npz", allow_pickle=False))
+    sd = fcv.synthetic.random_flow_state_dict(fcv.synthetic.FlowDims(), seed=int(g["weight_seed"]))
+    w = [sd[f"pre_lookahead_layer.{k}"] for k in ("conv1.weight", "conv1.bias", "conv2.weight",
+                                                  "conv2.bias")]
+    look = int(g["lookahead"])
+    out = F.pre_lookahead(torch.from_numpy(g["x"]), *w, look)
+    ref = torch.from_numpy(g["out_final"])
+    assert float((out - ref).abs().max()) <= 1e-5 * float(ref.abs().max())
+    out = F.pre_lookahead(torch.from_numpy(g["x_stream"]), *w, look,
+                          context=torch.from_numpy(g["context"]))
+    ref = torch.from_numpy(g["out_context"])
+    assert float((out - ref).abs().max()) <= 1e-5 * float(ref.abs().max())
