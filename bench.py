@@ -341,11 +341,13 @@ def _fresh_layouts(fcv, est, base, variants, K: int) -> dict:
     captured = captures()
 
     def timed(b, graph, bucketed):
+        # (wall ms per step, ms per step the calling thread spent inside the solve call)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         solve(b, graph, bucketed)
+        t1 = time.perf_counter()
         torch.cuda.synchronize()
-        return (time.perf_counter() - t0) * 1e3 / K
+        return (time.perf_counter() - t0) * 1e3 / K, (t1 - t0) * 1e3 / K
 
     replay, eager_bucketed, eager = [], [], []
     for v in variants:  # interleaved, so drift between the three falls on all of them
@@ -353,13 +355,15 @@ def _fresh_layouts(fcv, est, base, variants, K: int) -> dict:
         eager_bucketed.append(timed(v, False, True))
         eager.append(timed(v, False, False))
     new_captures = captures() - captured
-    med = lambda xs: sorted(xs)[len(xs) // 2]
+    med = lambda xs, i=0: round(sorted(x[i] for x in xs)[len(xs) // 2], 4)
     return {"request_groups": len(lanes), "capacities": [list(c) for c in _group_caps(fcv, base)],
             "layouts": len(variants), "rows": [v.rows for v in variants],
             "captures_during_replays": new_captures,
-            "replay_ms_per_step": round(med(replay), 4),
-            "eager_bucketed_ms_per_step": round(med(eager_bucketed), 4),
-            "eager_ms_per_step": round(med(eager), 4)}
+            "replay_ms_per_step": med(replay),
+            "eager_bucketed_ms_per_step": med(eager_bucketed),
+            "eager_ms_per_step": med(eager),
+            "host_ms_per_step": {"replay": med(replay, 1), "eager_bucketed": med(eager_bucketed, 1),
+                                 "eager": med(eager, 1)}}
 
 
 def fresh_layout_leg(fcv, est, batch, K: int, n_layouts: int = 4) -> dict:
@@ -373,7 +377,8 @@ def fresh_layout_leg(fcv, est, batch, K: int, n_layouts: int = 4) -> dict:
     import numpy as np
     out = {"what": "graph replay of new layouts in captured capacity buckets vs eager exact "
                    "plans", "timing": "median over the layouts; wall clock with "
-                   "torch.cuda.synchronize() on both sides"}
+                   "torch.cuda.synchronize() on both sides; host_ms_per_step: time the calling "
+                   "thread spends inside the solve call (enqueue, before the synchronize)"}
     rng = np.random.Generator(np.random.PCG64(7))
     variants = []
     for _ in range(200):

@@ -137,8 +137,14 @@ template <class E>
 struct pipeline_rows<E, std::void_t<decltype(E::kPipelineRows)>>
     : std::bool_constant<E::kPipelineRows> {};
 
+// workgroups per CU with the epilogue's row_info array in LDS as well
 template <class C, class Epi>
-__global__ __launch_bounds__(C::kThreads, C::kOcc) void gemm_kernel(
+constexpr int occupancy() {
+  return (160 * 1024) / (C::kLds + (Epi::kRowInfo ? C::BM * 4 : 0)) >= 2 ? C::kOcc : 1;
+}
+
+template <class C, class Epi>
+__global__ __launch_bounds__(C::kThreads, (occupancy<C, Epi>())) void gemm_kernel(
     const f16* __restrict__ A, int lda, const f16* __restrict__ W, int ldw, int M, int N, int K,
     Epi epi, const int32_t* __restrict__ m_live) {
   constexpr int BM = C::BM, BN = C::BN, TM = C::TM, TN = C::TN, BK = C::BK, S = C::STAGES;
