@@ -688,6 +688,10 @@ using Tile96x128 = TileCfg<96, 128, 1, 4>;
 using Tile96x128x3 = TileCfg<96, 128, 1, 4, 64, 3>;  // one workgroup per CU
 using Tile128x128x3 = TileCfg<128, 128, 2, 2, 64, 3>;  // one workgroup per CU
 using Tile32x128x4 = TileCfg<32, 128, 1, 4, 64, 4>;
+using Tile64x64x3 = TileCfg<64, 64, 2, 2, 64, 3>;    // three workgroups per CU
+using Tile64x64x4 = TileCfg<64, 64, 2, 2, 64, 4>;    // two workgroups per CU
+using Tile128x64x3 = TileCfg<128, 64, 2, 2, 64, 3>;  // two workgroups per CU
+using Tile64x128x3 = TileCfg<64, 128, 2, 2, 64, 3>;  // two workgroups per CU
 
 template <class C, class Epi>
 hipError_t launch_tile(const f16* A, int lda, const f16* W, int ldw, int M, int N, int K,
@@ -699,32 +703,71 @@ hipError_t launch_tile(const f16* A, int lda, const f16* W, int ldw, int M, int 
   return hipGetLastError();
 }
 
-// Tile choice: estimated time = (tiles per CU, rounded up) x tile area / per-CU rate.  The
-// rates are fitted so the estimate picks the fastest shape measured for the block GEMMs
-// (N = 1024, 2048, 3072 at ~4.6k and ~9.2k rows, production epilogues): 128x128 runs two
-// workgroups per CU, which its rate includes; 160x256 runs one wave per SIMD, so it rates low
-// although it fills more CUs; 32x128 is rated low so it only wins when the larger shapes leave
-// most CUs idle, as for the 128-column output projection.  96x128 (four 96x32 waves, two
-// workgroups per CU) sits between 32x128 below and 192x256 above: it wins for the 1024-column
-// GEMMs from ~2k to ~6k rows (a request group's share of a batch) and for FF1 and QKV at one to
-// three thousand rows (a single request or a short stream); a sweep of the four block GEMMs
-// over 1.1k-9.3k rows with every shape forced found the estimate's pick within 1 % of the
-// fastest shape, except QKV at 1.1k rows (128x128, 6 % slower than 96x128) and at 6.2k rows
-// (4 %).  The choice only changes which rows
-// and columns share a workgroup: every output element still accumulates its K slices in the
-// same order, so results are bitwise identical for every tile shape (batch invariance holds).
+// Tile choice for larger launches: estimated time = (tiles per CU, rounded up) x tile area /
+// per-CU rate.  The rates are fitted so the estimate picks the fastest shape measured for the
+// block GEMMs (N = 1024, 2048, 3072 at ~4.6k and ~9.2k rows, production epilogues): 128x128
+// runs two workgroups per CU, which its rate includes; 160x256 runs one wave per SIMD, so it
+// rates low although it fills more CUs; 32x128 is rated low so it only wins when the larger
+// shapes leave most CUs idle.  96x128 (four 96x32 waves, two workgroups per CU) sits below
+// 192x256: it wins for the 1024-column GEMMs from ~2.5k to ~6k rows (a request group's share
+// of a batch) and for FF1 and QKV at ~1.3k-3k rows; a sweep of the four block GEMMs over
+// 1.1k-9.3k rows with every shape forced found the estimate's pick within 1 % of the fastest
+// shape, except at 6.2k rows (QKV, 4 %).
+//
+// Small launches (one or two requests, up to ~3k rows) follow a measured table instead.  A K
+// loop there is latency-bound, and two or three 64-column workgroups per CU (64x64 with four
+// ring stages up to 256 tiles and three above, 128x64 and 64x128 with three) overlap their copy
+// latencies better than one larger tile does, up to where the larger tiles fill one round of
+// CUs with their three-stage form.  The table is the fastest shape per output width measured
+// in eager 22-block solves (weights streamed from HBM as in production) at 340-3090 rows with
+// every shape forced; its pick is within 3 % of the fastest forced shape at every measured size
+// but one (QKV at ~980 rows, 8 %), and the four GEMMs of a block take 12-16 % less time at
+// 340-1170 rows than the estimate's pick.  The choice only changes which rows and columns share
+// a workgroup: every output element still accumulates its K slices in the same order, so
+// results are bitwise identical for every tile shape (batch invariance holds).
 constexpr int kCus = 256;
-constexpr int kTileShapes = 8;
+constexpr int kTileShapes = 11;
 constexpr int kTileShape[kTileShapes][2] = {{256, 256}, {192, 256}, {128, 256}, {256, 128},
-                                            {128, 128}, {32, 128},  {160, 256}, {96, 128}};
-constexpr float kTileRate[kTileShapes] = {1.0f, 0.97f, 0.80f, 0.78f, 0.85f, 0.45f, 0.75f, 0.66f};
+                                            {128, 128}, {32, 128},  {160, 256}, {96, 128},
+                                            {64, 64},   {128, 64},  {64, 128}};
+// 0: chosen from the small-launch table only
+constexpr float kTileRate[kTileShapes] = {1.0f, 0.97f, 0.80f, 0.78f, 0.85f, 0.45f, 0.75f, 0.66f,
+                                          0.0f, 0.0f,  0.0f};
+constexpr int kTile128x128 = 4, kTile96x128 = 7, kTile64x64 = 8, kTile128x64 = 9, kTile64x128 = 10;
+
+inline long tile_count(int M, int N, int bm, int bn) { return (long)((M + bm - 1) / bm) * (N / bn); }
+
+// (largest M, shape) steps of the small-launch table for one output width
+struct SmallStep {
+  int max_m, shape;
+};
+constexpr SmallStep kSmall1024[] = {  // output projection and FF2 (K 1024 and 2048)
+    {1440, kTile64x64}, {2100, kTile128x64}, {3072, kTile96x128}};
+constexpr SmallStep kSmall2048[] = {  // FF1
+    {600, kTile64x64}, {1000, kTile128x64}, {1536, kTile96x128}, {2048, kTile128x128},
+    {2200, kTile128x64}};
+constexpr SmallStep kSmall3072[] = {  // QKV
+    {400, kTile64x64}, {1200, kTile128x64}, {1440, kTile64x128}, {2100, kTile96x128}};
+
+template <int L>
+inline int small_step(const SmallStep (&steps)[L], int M) {
+  for (const SmallStep& s : steps)
+    if (M <= s.max_m) return s.shape;
+  return -1;
+}
 
 inline int choose_tile(int M, int N) {
+  int small = -1;
+  if (N == 1024) small = small_step(kSmall1024, M);
+  else if (N == 2048) small = small_step(kSmall2048, M);
+  else if (N == 3072) small = small_step(kSmall3072, M);
+  else if (N < 1024 && tile_count(M, N, 64, 64) <= 640) small = kTile64x64;  // output projection
+  if (small >= 0) return small;
   int best = 4;
   float best_t = 3.0e38f;
   for (int c = 0; c < kTileShapes; ++c) {
     const int bm = kTileShape[c][0], bn = kTileShape[c][1];
-    if (N % bn != 0) continue;
+    if (N % bn != 0 || kTileRate[c] <= 0.0f) continue;
     const long tiles = (long)((M + bm - 1) / bm) * (N / bn);
     const long per_cu = (tiles + kCus - 1) / kCus;
     const float t = (float)per_cu * bm * bn / kTileRate[c];
@@ -764,6 +807,14 @@ hipError_t launch(const f16* A, int lda, const f16* W, int ldw, int M, int N, in
         return launch_tile<Tile32x128x4>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
       return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
     case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case kTile64x64:
+      if (tile_count(M, N, 64, 64) <= kCus)
+        return launch_tile<Tile64x64x4>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+      return launch_tile<Tile64x64x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case kTile128x64:
+      return launch_tile<Tile128x64x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+    case kTile64x128:
+      return launch_tile<Tile64x128x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
     case 7:
       // where the tiles fit one round of CUs, a third ring stage gives each copy more lead (the
       // tile then holds a CU alone); with more tiles the two-stage form's two per CU win

@@ -458,7 +458,7 @@ def test_batch_invariance_and_determinism(fcv, stress2):
 
 def test_every_gemm_tile_shape_gives_the_same_bits(fcv, stress2, monkeypatch):
     """The GEMM tile shape only decides which rows and columns share a workgroup, never an
-    element's K order.  Forcing each of the eight shapes (FCV_GEMM_TILE, wherever it divides
+    element's K order.  Forcing each of the eleven shapes (FCV_GEMM_TILE, wherever it divides
     the output width) reproduces the default choice bit for bit, with the full and the
     chunk-causal mask and with one shared t and one t per document."""
     sd, est = stress2
@@ -468,7 +468,7 @@ def test_every_gemm_tile_shape_gives_the_same_bits(fcv, stress2, monkeypatch):
         for t in (torch.tensor([0.42]), t_doc):
             monkeypatch.delenv("FCV_GEMM_TILE", raising=False)
             ref = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming)
-            for shape in range(8):
+            for shape in range(11):
                 say(f"[tiles] streaming={streaming} n_t={t.numel()} shape {shape}")
                 monkeypatch.setenv("FCV_GEMM_TILE", str(shape))
                 got = est.forward_packed(x, mu, cond, spks, t, lengths, streaming=streaming)
