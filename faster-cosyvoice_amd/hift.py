@@ -29,6 +29,14 @@ def _ceil(v: int, m: int) -> int:
     return (v + m - 1) // m * m
 
 
+# Smallest capacity (Mel frames of one packed call) whose call replays its captured graph when
+# the caller leaves ``graph`` to the vocoder.  The eager call is one C-ABI call that enqueues the
+# launch sequence faster than the GPU drains it, so a replay saves host time but no device time:
+# on one MI355X a 68-frame streaming chunk took 2.31 ms either way, and config 3's packed
+# groups 19.4 ms either way.  Small calls (streaming chunks) therefore launch eagerly.
+HIFT_GRAPH_MIN_FRAMES = 1024
+
+
 def capacity_bucket(frames: int, n_docs: int) -> tuple[int, int]:
     """The capacity a packed vocoder call of ``frames`` Mel frames in ``n_docs`` requests is
     run in: frames rounded up to m * 2^e with m in 8..15 (at most 12.5 % above, at least 64),
@@ -257,10 +265,11 @@ class HiFTVocoder:
         return bufs
 
     def _run(self, lane: list, mels: list[torch.Tensor], fin: list[bool], return_source: bool,
-             stream: int, graph: bool = True) -> tuple[list, list]:
+             stream: int, graph: bool | None = None) -> tuple[list, list]:
         """Packed calls of at most HIFT_MAX_DOCS requests on ``lane``, enqueued on ``stream``.
         Each call runs in its capacity bucket (``capacity_bucket``) from the lane's buffers for
-        that capacity; with ``graph`` the capacity's captured graph replays it."""
+        that capacity; with ``graph`` the capacity's captured graph replays it (None: for
+        capacities of at least ``HIFT_GRAPH_MIN_FRAMES`` frames)."""
         h = lane[0]
         speech_all, source_all = [], []
         for g0 in range(0, len(mels), _lib.HIFT_MAX_DOCS):
@@ -271,6 +280,7 @@ class HiFTVocoder:
             f0_frames = [t if f else t - 3 for t, f in zip(frames, gfin)]
             src_len = [t * self.dims.upsample_scale for t in f0_frames]
             cap = capacity_bucket(sum(frames), len(group))
+            replay = graph if graph is not None else cap[0] >= HIFT_GRAPH_MIN_FRAMES
             bufs = self._buffers(lane, cap, return_source)
             off = 0
             for m in group:
@@ -289,7 +299,7 @@ class HiFTVocoder:
             _lib.check(self._lib.fcv_hift_inference_capacity(
                 h, bufs["mel"].data_ptr(), fr, fl, len(group), cap[0], cap[1],
                 bufs["speech"].data_ptr(), source.data_ptr() if source is not None else None,
-                lane[1].data_ptr(), lane[1].numel(), int(bool(graph)), stream))
+                lane[1].data_ptr(), lane[1].numel(), int(bool(replay)), stream))
             # the buffers are the lane's: the next call writes them again
             speech = bufs["speech"][:sum(samples)].clone()
             off = 0
@@ -308,7 +318,7 @@ class HiFTVocoder:
     def inference_batched(self, mels: Sequence[torch.Tensor],
                           finalize_list: Sequence[bool] | None = None,
                           return_source: bool = False, concurrency: int | None = None,
-                          graph: bool = True):
+                          graph: bool | None = None):
         """Vocode requests of different lengths in packed passes.  ``mels``: each ``[80, T]``
         or ``[1, 80, T]``.  Returns one ``[1, N]`` fp32 waveform per request (and the
         ``[1, 1, L]`` sources with ``return_source``).  Each waveform equals what
@@ -321,7 +331,9 @@ class HiFTVocoder:
 
         Each call runs in a capacity bucket (``capacity_bucket``); with ``graph`` the launch
         sequence is captured on a bucket's second call and replayed for every later layout in
-        it (fcv_hift_inference_capacity), bit-identical to an eager call."""
+        it (fcv_hift_inference_capacity), bit-identical to an eager call.  ``graph=None`` (the
+        default) replays for capacities of at least ``HIFT_GRAPH_MIN_FRAMES`` frames and
+        launches smaller calls eagerly."""
         self._require()
         mels = [m.reshape(m.shape[-2], m.shape[-1]) for m in mels]
         if not mels:

@@ -7,6 +7,9 @@ and its second captures the graph, since a capture costs more than one eager run
 ``solve_euler_batched`` keeps the reference's padded signature for callers that hand it
 ``[B,80,T]`` tensors and a padding mask.
 
+``use_graph`` left to the solver replays graphs for request groups of at least
+``GRAPH_MIN_ROWS`` capacity rows and launches smaller ones eagerly (see there).
+
 By default a solve plans its layout into a capacity bucket (``capacity_bucket``): the
 kernels read the layout from device memory, so the graph captured for a bucket replays for
 every later layout that fits it (a streaming step or a new batch composition), where an exact
@@ -63,6 +66,14 @@ def capacity_bucket(rows: int, n_docs: int) -> tuple[int, int]:
 
 
 _BUFFER_SETS = 4  # solver buffer sets kept per runner: one per graph its handle can pool
+
+# Smallest capacity (packed CFG rows of one request group) whose solve replays its hipGraph
+# when the caller leaves ``use_graph`` to the solver.  An eager solve is one C-ABI call that
+# enqueues the whole step from C++ faster than the GPU drains it, so a replay saves host time
+# (0.10 against 0.44-0.49 ms per step for one request) but no device time; on one MI355X the
+# replayed step was 2-4 % slower than the same kernels launched eagerly at 760-1100 rows and
+# 1 % faster at config 3's request groups (~4.6k rows each).
+GRAPH_MIN_ROWS = 4096
 
 
 def _solver_buffers(runner: _PackedRunner, dims, rows_cap: int,
@@ -140,13 +151,15 @@ def request_groups(lengths: Sequence[int], n_groups: int) -> list[list[int]]:
 
 def _solve_on(runner: _PackedRunner, dims, noise: torch.Tensor, mu: torch.Tensor,
               cond: torch.Tensor, spks: torch.Tensor, lengths: list[int], t_arr, dt_arr,
-              n_steps: int, cfg_rate: float, streaming: bool, use_graph: bool,
+              n_steps: int, cfg_rate: float, streaming: bool, use_graph: bool | None,
               stream: torch.cuda.Stream, bucketed: bool,
               schedule: torch.Tensor) -> torch.Tensor:
     """One packed CFG solve on ``runner``, enqueued on ``stream`` (the caller orders it).  It
     reads its modulation rows from ``schedule`` (filled by ``fcv_dit_schedule``)."""
     rc, b = sum(lengths), len(lengths)
     capacity = capacity_bucket(2 * rc, 2 * b) if bucketed else None
+    if use_graph is None:
+        use_graph = (capacity or (2 * rc, 2 * b))[0] >= GRAPH_MIN_ROWS
     with torch.cuda.stream(stream):
         runner.plan(lengths + lengths, streaming, capacity)
         # persistent solver buffers: stable pointers let a captured graph be replayed; the
@@ -171,7 +184,7 @@ def _solve_on(runner: _PackedRunner, dims, noise: torch.Tensor, mu: torch.Tensor
 def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.Tensor,
                        cond: torch.Tensor, spks: torch.Tensor, lengths: Sequence[int],
                        n_steps: int = 10, cfg_rate: float = 0.7, streaming: bool = False,
-                       use_graph: bool = True, concurrency: int | None = None,
+                       use_graph: bool | None = None, concurrency: int | None = None,
                        bucketed: bool = True) -> torch.Tensor:
     """CFG Euler solve on packed request rows.
 
@@ -191,6 +204,8 @@ def solve_euler_packed(estimator: DiTEstimator, noise: torch.Tensor, mu: torch.T
 
     ``bucketed`` plans each group into its capacity bucket (``capacity_bucket``), so a new
     layout in a bucket that has been captured replays its graph; False plans the exact layout.
+    ``use_graph``: True replays graphs, False launches eagerly, None (default) replays them for
+    groups of at least ``GRAPH_MIN_ROWS`` capacity rows.  Results are bit-identical either way.
     """
     lengths = [int(n) for n in lengths]
     rc = sum(lengths)

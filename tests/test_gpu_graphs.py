@@ -52,7 +52,7 @@ def test_one_graph_serves_every_layout_in_its_capacity(fcv, est2, streaming):
     sequence = [("A", 0), ("A", 1), ("B", 1), ("C", 1), ("C", 2), ("B", 2), ("A", 2), ("C", 2)]
     for name, captures in sequence:
         say(f"[capacity] streaming={streaming}: graph solve {name}")
-        got = _solve(fcv, est2, batches[name], streaming)
+        got = _solve(fcv, est2, batches[name], streaming, use_graph=True)
         assert torch.equal(got, exact[name]), name
         assert est2.graph_stats()[1] - c0 == captures, name
 
@@ -72,13 +72,13 @@ def test_graph_pool_keeps_four_capacities(fcv):
     _, c0 = est2.graph_stats()
     for i, b in enumerate(batches):
         say(f"[pool] capacity {caps[i]}: first, second solve")
-        assert torch.equal(_solve(fcv, est2, b, False), exact[i])
-        assert torch.equal(_solve(fcv, est2, b, False), exact[i])
+        assert torch.equal(_solve(fcv, est2, b, False, use_graph=True), exact[i])
+        assert torch.equal(_solve(fcv, est2, b, False, use_graph=True), exact[i])
     pooled, c = est2.graph_stats()
     assert pooled == 4 and c - c0 == 5
     for i in (1, 2, 3, 4):  # still pooled: replays
-        assert torch.equal(_solve(fcv, est2, batches[i], False), exact[i])
+        assert torch.equal(_solve(fcv, est2, batches[i], False, use_graph=True), exact[i])
     assert est2.graph_stats()[1] - c0 == 5
     # the first capacity was dropped: its next solve is its first sight again (eager)
-    assert torch.equal(_solve(fcv, est2, batches[0], False), exact[0])
+    assert torch.equal(_solve(fcv, est2, batches[0], False, use_graph=True), exact[0])
     assert est2.graph_stats()[1] - c0 == 5
