@@ -257,18 +257,18 @@ class DiTEstimator(nn.Module, _PackedRunner):
             raise ValueError("DiTEstimator runs on a GPU device")
         lib = _lib.load()
         dev, D, L = self.device, self.dim, self.depth
-        bf = lambda t: t.detach().to(device=dev, dtype=torch.float16).contiguous()
+        h16 = lambda t: t.detach().to(device=dev, dtype=torch.float16).contiguous()
         f32 = lambda t: t.detach().to(device=dev, dtype=torch.float32).contiguous()
         blocks = self.transformer_blocks
 
         out: dict[str, torch.Tensor] = {}
-        out["temb_w1"] = bf(self.time_embed.time_mlp[0].weight)
+        out["temb_w1"] = h16(self.time_embed.time_mlp[0].weight)
         out["temb_b1"] = f32(self.time_embed.time_mlp[0].bias)
-        out["temb_w2"] = bf(self.time_embed.time_mlp[2].weight)
+        out["temb_w2"] = h16(self.time_embed.time_mlp[2].weight)
         out["temb_b2"] = f32(self.time_embed.time_mlp[2].bias)
 
         ada_w = [b.attn_norm.linear.weight for b in blocks] + [self.norm_out.linear.weight]
-        out["ada_w"] = bf(torch.cat([w.detach().float().cpu() for w in ada_w]))
+        out["ada_w"] = h16(torch.cat([w.detach().float().cpu() for w in ada_w]))
         ada_b = []
         for b in blocks:
             bias = b.attn_norm.linear.bias.detach().float().cpu().clone().view(6, D)
@@ -280,7 +280,7 @@ class DiTEstimator(nn.Module, _PackedRunner):
         ada_b.append(fin.reshape(-1))
         out["ada_b"] = f32(torch.cat(ada_b))
 
-        out["in_w"] = bf(self.input_embed.proj.weight)
+        out["in_w"] = h16(self.input_embed.proj.weight)
         out["in_b"] = f32(self.input_embed.proj.bias)
         groups = self.dims.conv_groups
         cpg = D // groups
@@ -289,20 +289,20 @@ class DiTEstimator(nn.Module, _PackedRunner):
             w = seq[0].weight.detach().float().cpu()  # (C, C/G, K)
             taps = w.shape[-1]
             w = w.view(groups, cpg, cpg, taps).permute(0, 3, 1, 2)  # (G, K, co, ci)
-            out[f"conv{i}_w"] = bf(w.contiguous())
+            out[f"conv{i}_w"] = h16(w.contiguous())
             out[f"conv{i}_b"] = f32(seq[0].bias)
 
-        out["qkv_w"] = bf(torch.stack([torch.cat([b.attn.to_q.weight, b.attn.to_k.weight,
+        out["qkv_w"] = h16(torch.stack([torch.cat([b.attn.to_q.weight, b.attn.to_k.weight,
                                                   b.attn.to_v.weight]).detach().float().cpu()
                                        for b in blocks]))
         out["qkv_b"] = f32(torch.stack([torch.cat([b.attn.to_q.bias, b.attn.to_k.bias,
                                                    b.attn.to_v.bias]).detach().float().cpu()
                                         for b in blocks]))
-        out["out_w"] = bf(torch.stack([b.attn.to_out[0].weight.detach().float().cpu() for b in blocks]))
+        out["out_w"] = h16(torch.stack([b.attn.to_out[0].weight.detach().float().cpu() for b in blocks]))
         out["out_b"] = f32(torch.stack([b.attn.to_out[0].bias.detach().float().cpu() for b in blocks]))
-        out["ff1_w"] = bf(torch.stack([b.ff.ff[0][0].weight.detach().float().cpu() for b in blocks]))
+        out["ff1_w"] = h16(torch.stack([b.ff.ff[0][0].weight.detach().float().cpu() for b in blocks]))
         out["ff1_b"] = f32(torch.stack([b.ff.ff[0][0].bias.detach().float().cpu() for b in blocks]))
-        out["ff2_w"] = bf(torch.stack([b.ff.ff[2].weight.detach().float().cpu() for b in blocks]))
+        out["ff2_w"] = h16(torch.stack([b.ff.ff[2].weight.detach().float().cpu() for b in blocks]))
         out["ff2_b"] = f32(torch.stack([b.ff.ff[2].bias.detach().float().cpu() for b in blocks]))
 
         mel = self.dims.mel_dim
@@ -310,7 +310,7 @@ class DiTEstimator(nn.Module, _PackedRunner):
         pw[:mel] = self.proj_out.weight.detach().float().cpu()
         pb = torch.zeros(128)
         pb[:mel] = self.proj_out.bias.detach().float().cpu()
-        out["proj_w"] = bf(pw)
+        out["proj_w"] = h16(pw)
         out["proj_b"] = f32(pb)
 
         cos, sin = rope_tables(self.max_pos, self.dim_head, self.rope_dim)
