@@ -689,8 +689,9 @@ using Tile96x128x3 = TileCfg<96, 128, 1, 4, 64, 3>;  // one workgroup per CU
 using Tile128x128x3 = TileCfg<128, 128, 2, 2, 64, 3>;  // one workgroup per CU
 using Tile32x128x4 = TileCfg<32, 128, 1, 4, 64, 4>;
 using Tile64x64x3 = TileCfg<64, 64, 2, 2, 64, 3>;    // three workgroups per CU
-using Tile64x64x4 = TileCfg<64, 64, 2, 2, 64, 4>;    // two workgroups per CU
+using Tile64x64x5 = TileCfg<64, 64, 2, 2, 64, 5>;    // two workgroups per CU
 using Tile128x64x3 = TileCfg<128, 64, 2, 2, 64, 3>;  // two workgroups per CU
+using Tile128x64x4 = TileCfg<128, 64, 2, 2, 64, 4>;  // one workgroup per CU
 using Tile64x128x3 = TileCfg<64, 128, 2, 2, 64, 3>;  // two workgroups per CU
 
 template <class C, class Epi>
@@ -715,16 +716,18 @@ hipError_t launch_tile(const f16* A, int lda, const f16* W, int ldw, int M, int 
 // shape, except at 6.2k rows (QKV, 4 %).
 //
 // Small launches (one or two requests, up to ~3k rows) follow a measured table instead.  A K
-// loop there is latency-bound, and two or three 64-column workgroups per CU (64x64 with four
-// ring stages up to 256 tiles and three above, 128x64 and 64x128 with three) overlap their copy
-// latencies better than one larger tile does, up to where the larger tiles fill one round of
-// CUs with their three-stage form.  The table is the fastest shape per output width measured
-// in eager 22-block solves (weights streamed from HBM as in production) at 340-3090 rows with
-// every shape forced; its pick is within 3 % of the fastest forced shape at every measured size
-// but one (QKV at ~980 rows, 8 %), and the four GEMMs of a block take 12-16 % less time at
-// 340-1170 rows than the estimate's pick.  The choice only changes which rows and columns share
-// a workgroup: every output element still accumulates its K slices in the same order, so
-// results are bitwise identical for every tile shape (batch invariance holds).
+// loop there is bound by the copies' latency, so what counts is how many slices are in flight
+// per CU: 64x64 tiles with five ring stages (two per CU) while two per CU hold every tile and
+// three stages (three per CU) above, 128x64 with four stages (one per CU) up to ~one round and
+// three (two per CU) above, and 64x128 with three.  The larger tiles take over where they fill
+// one round of CUs with their three-stage form.  The table is the fastest shape per output
+// width measured in eager 22-block solves (weights streamed from HBM as in production) at the
+// capacities one request plans into (340-3090 rows) with every shape and ring depth forced;
+// its pick is within 3 % of the fastest at every measured size, and the four GEMMs of a block
+// take 12-20 % less time at 340-1170 rows than the estimate's pick.  The choice only changes
+// which rows and columns share a workgroup: every output element still accumulates its K
+// slices in the same order, so results are bitwise identical for every tile shape (batch
+// invariance holds).
 constexpr int kCus = 256;
 constexpr int kTileShapes = 11;
 constexpr int kTileShape[kTileShapes][2] = {{256, 256}, {192, 256}, {128, 256}, {256, 128},
@@ -742,12 +745,13 @@ struct SmallStep {
   int max_m, shape;
 };
 constexpr SmallStep kSmall1024[] = {  // output projection and FF2 (K 1024 and 2048)
-    {1440, kTile64x64}, {2100, kTile128x64}, {3072, kTile96x128}};
+    {1024, kTile64x64}, {2100, kTile128x64}, {3072, kTile96x128}};
 constexpr SmallStep kSmall2048[] = {  // FF1
     {600, kTile64x64}, {1000, kTile128x64}, {1536, kTile96x128}, {2048, kTile128x128},
     {2200, kTile128x64}};
 constexpr SmallStep kSmall3072[] = {  // QKV
-    {400, kTile64x64}, {1200, kTile128x64}, {1440, kTile64x128}, {2100, kTile96x128}};
+    {400, kTile64x64}, {850, kTile128x64}, {1000, kTile64x128}, {1200, kTile128x64},
+    {1440, kTile64x128}, {2100, kTile96x128}};
 
 template <int L>
 inline int small_step(const SmallStep (&steps)[L], int M) {
@@ -808,10 +812,14 @@ hipError_t launch(const f16* A, int lda, const f16* W, int ldw, int M, int N, in
       return launch_tile<Tile32x128>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
     case 6: return launch_tile<Tile160x256>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
     case kTile64x64:
-      if (tile_count(M, N, 64, 64) <= kCus)
-        return launch_tile<Tile64x64x4>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
+      // five ring stages while two per CU hold every tile, three (three per CU) above
+      if (tile_count(M, N, 64, 64) <= 2 * kCus)
+        return launch_tile<Tile64x64x5>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
       return launch_tile<Tile64x64x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
     case kTile128x64:
+      // four stages (one per CU) up to ~one round, three (two per CU) above
+      if (tile_count(M, N, 128, 64) <= 288)
+        return launch_tile<Tile128x64x4>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
       return launch_tile<Tile128x64x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
     case kTile64x128:
       return launch_tile<Tile64x128x3>(A, lda, W, ldw, M, N, K, epi, stream, m_live);
