@@ -765,7 +765,7 @@ inline int choose_tile(int M, int N) {
   if (N == 1024) small = small_step(kSmall1024, M);
   else if (N == 2048) small = small_step(kSmall2048, M);
   else if (N == 3072) small = small_step(kSmall3072, M);
-  else if (N < 1024 && tile_count(M, N, 64, 64) <= 640) small = kTile64x64;  // output projection
+  else if (N < 1024 && M <= 3072) small = kTile64x64;  // output projection (128 columns)
   if (small >= 0) return small;
   int best = 4;
   float best_t = 3.0e38f;
