@@ -137,6 +137,12 @@ template <class E>
 struct pipeline_rows<E, std::void_t<decltype(E::kPipelineRows)>>
     : std::bool_constant<E::kPipelineRows> {};
 
+// Whether an epilogue writes some tiles in the accumulator's own lane layout (finish_direct).
+template <class E, class = void>
+struct direct_layout : std::false_type {};
+template <class E>
+struct direct_layout<E, std::void_t<decltype(&E::finish_direct)>> : std::true_type {};
+
 // workgroups per CU with the epilogue's row_info array in LDS as well
 template <class C, class Epi>
 constexpr int occupancy() {
@@ -215,7 +221,8 @@ __global__ __launch_bounds__(C::kThreads, (occupancy<C, Epi>())) void gemm_kerne
   constexpr int WCOLS = TN * 32;
   constexpr int LANES_PER_ROW = WCOLS / 4;
   const int col_base = n0 + wn0;
-  const bool direct = epi.direct(col_base);
+  bool direct = false;
+  if constexpr (direct_layout<Epi>::value) direct = epi.direct(col_base);
   const int rc = (lane % LANES_PER_ROW) * 4;
   Col scol{};
   Col dcol[TN][4];
@@ -327,6 +334,7 @@ __global__ __launch_bounds__(C::kThreads, (occupancy<C, Epi>())) void gemm_kerne
   using Ctx = typename Epi::Ctx;
   constexpr int PITCH = WCOLS + 4;  // floats
   static_assert(C::kWaves * 32 * PITCH * 4 <= (int)sizeof(smem), "epilogue staging");
+  if constexpr (direct_layout<Epi>::value) {
   if (direct) {
     // direct-layout tiles (V^T) read nothing per row
 #pragma unroll
@@ -339,11 +347,12 @@ __global__ __launch_bounds__(C::kThreads, (occupancy<C, Epi>())) void gemm_kerne
           const f32x4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                            acc[i][j][4 * g + 3]};
           const int c = col_base + j * 32 + g * 8 + fh * 4;
-          epi.finish(v, epi.blank(dcol[j][g]), dcol[j][g], row, c, M);
+          epi.finish_direct(v, dcol[j][g], row, c, M);
         }
       }
     }
     return;
+  }
   }
   __syncthreads();  // every wave is done reading the operand ring
   float* stg = reinterpret_cast<float*>(smem) + wave * 32 * PITCH;
@@ -402,7 +411,7 @@ __global__ __launch_bounds__(C::kThreads, (occupancy<C, Epi>())) void gemm_kerne
       for (int p = 0; p < PASSES; ++p) {
         const int r = p * ROWS_PER_PASS + rr;
         const Ctx x = kLoads ? cx[p] : epi.blank(scol);
-        epi.finish(v[p], x, scol, m0 + wm0 + i * 32 + r, col, M);
+        epi.template finish<kLoads>(v[p], x, scol, m0 + wm0 + i * 32 + r, col, M);
       }
       if constexpr (kLoads && kAhead) {
         if (i + 1 < TM) {
@@ -471,6 +480,7 @@ struct EpiBiasF32F16 {
   __device__ Col column(int col) const { return {ld4(bias + col)}; }
   static constexpr bool kRowInfo = false;
   __device__ Ctx prepare(int, int, int, const Col&, int) const { return {}; }
+  template <bool kRowCtx>
   __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
     const f16x4 yb = f2h4(y.x, y.y, y.z, y.w);
@@ -495,6 +505,7 @@ struct EpiBiasF32 {
   }
   static constexpr bool kRowInfo = false;
   __device__ Ctx prepare(int, int, int, const Col&, int) const { return {}; }
+  template <bool kRowCtx>
   __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
     if (row >= M || col >= n_valid) return;
@@ -521,6 +532,7 @@ struct EpiBiasF32RowMap {
   __device__ Ctx prepare(int row, int, int M, const Col&, int info) const {
     return {row < M ? info : -1};
   }
+  template <bool kRowCtx>
   __device__ void finish(const f32x4& v, const Ctx& x, const Col& c, int, int col, int) const {
     const float4 y = add4(v, c.b);
     if (x.dst < 0 || col >= n_valid) return;
@@ -540,6 +552,7 @@ struct EpiBiasSiluF16 {
   __device__ Col column(int col) const { return {ld4(bias + col)}; }
   static constexpr bool kRowInfo = false;
   __device__ Ctx prepare(int, int, int, const Col&, int) const { return {}; }
+  template <bool kRowCtx>
   __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
     const f16x4 yb = f2h4(silu(y.x), silu(y.y), silu(y.z), silu(y.w));
@@ -560,6 +573,7 @@ struct EpiBiasGeluF16 {
   __device__ Col column(int col) const { return {ld4(bias + col)}; }
   static constexpr bool kRowInfo = false;
   __device__ Ctx prepare(int, int, int, const Col&, int) const { return {}; }
+  template <bool kRowCtx>
   __device__ void finish(const f32x4& v, const Ctx&, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
     const f16x4 yb = f2h4(gelu_tanh(y.x), gelu_tanh(y.y), gelu_tanh(y.z), gelu_tanh(y.w));
@@ -602,6 +616,7 @@ struct EpiGatedResidual {
     x.x = buffer_ld4(buffer_over(h, (uint32_t)M * ldh * 4), (uint32_t)(row * ldh + col) * 4);
     return x;
   }
+  template <bool kRowCtx>
   __device__ void finish(const f32x4& v, const Ctx& x, const Col& c, int row, int col, int M) const {
     const float4 y = add4(v, c.b);
     const float4 r = {fmaf(x.g.x, y.x, x.x.x), fmaf(x.g.y, y.y, x.x.y), fmaf(x.g.z, y.z, x.x.z),
@@ -638,7 +653,7 @@ struct EpiQkvRope {
   __device__ int row_info(int row) const { return min(pos[row], max_pos - 1); }
   __device__ Ctx prepare(int row, int col, int M, const Col&, int info) const {
     Ctx c = {{1.0f, 1.0f}, {0.0f, 0.0f}};  // identity rotation where no angle is loaded
-    const int cc = col % dim;
+    const int cc = col >= dim ? col - dim : col;  // column in q or k (used when col < 2 dim)
     if (col < 2 * dim && row < M && cc < rope_dim) {
       // angles of the interleaved pairs (cc, cc+1), (cc+2, cc+3)
       const long t = (long)info * (rope_dim >> 1) + (cc >> 1);
@@ -647,33 +662,44 @@ struct EpiQkvRope {
     }
     return c;
   }
+  // V^T tiles (columns >= 2 dim) keep the accumulator lane layout: vt[head][d + e][row], 32
+  // lanes = 32 consecutive rows; rows in [M, rp) get finite copies of row M-1
+  __device__ void finish_direct(const f32x4& v, const Col& cb, int row, int col, int) const {
+    const float4 y = add4(v, cb.b);
+    const int c = col - 2 * dim;
+    const int head = c >> 6, d = c & 63;
+    const f16x4 v4 = f2h4(y.x, y.y, y.z, y.w);
+    if (row >= rp) return;
+    f16* dst = vt + ((long)head * 64 + d) * rp + row;
+    dst[0] = v4[0];
+    dst[rp] = v4[1];
+    dst[2 * rp] = v4[2];
+    dst[3 * rp] = v4[3];
+  }
+  // q and k tiles (staged row-major): a wave's columns (at most 64, aligned) lie in one head, so
+  // which, head and d are the same in every call of a lane.  kRowCtx: the tile's columns read
+  // rotary angles (row_loads); without them no column of the tile rotates.
+  template <bool kRowCtx>
   __device__ void finish(const f32x4& v, const Ctx& cx, const Col& cb, int row, int col,
                          int M) const {
     float4 y = add4(v, cb.b);
-    const int which = col / dim;  // 0 q, 1 k, 2 v
+    // 0 q, 1 k; the same for every lane of a wave (its columns lie in one head), made scalar so
+    // the store's buffer descriptor is built once in scalar registers
+    const int which = __builtin_amdgcn_readfirstlane(col >= dim ? 1 : 0);
     const int c = col - which * dim;
     const int head = c >> 6, d = c & 63;
-    if (which == 2) {
-      // V transposed: vt[head][d + e][row]; rows in [M, rp) get finite copies of row M-1
-      const f16x4 v4 = f2h4(y.x, y.y, y.z, y.w);
-      const f16 v0 = v4[0], v1 = v4[1], v2 = v4[2], v3 = v4[3];
-      if (row >= rp) return;
-      vt[((long)head * 64 + d) * rp + row] = v0;
-      vt[((long)head * 64 + d + 1) * rp + row] = v1;
-      vt[((long)head * 64 + d + 2) * rp + row] = v2;
-      vt[((long)head * 64 + d + 3) * rp + row] = v3;
-      return;
+    if constexpr (kRowCtx) {
+      // (a, b) -> (a cos - b sin, b cos + a sin) on the rotated columns (c < rope_dim)
+      const float a0 = y.x, b0 = y.y, a1 = y.z, b1 = y.w;
+      const float4 yr = {a0 * cx.cs.x - b0 * cx.sn.x, b0 * cx.cs.x + a0 * cx.sn.x,
+                         a1 * cx.cs.y - b1 * cx.sn.y, b1 * cx.cs.y + a1 * cx.sn.y};
+      if (c < rope_dim) y = yr;
     }
-    // (a, b) -> (a cos - b sin, b cos + a sin) on the rotated columns; the angles are only
-    // loaded there, so the other columns select the unrotated values
-    const float a0 = y.x, b0 = y.y, a1 = y.z, b1 = y.w;
-    const float4 yr = {a0 * cx.cs.x - b0 * cx.sn.x, b0 * cx.cs.x + a0 * cx.sn.x,
-                       a1 * cx.cs.y - b1 * cx.sn.y, b1 * cx.cs.y + a1 * cx.sn.y};
-    if (c < rope_dim) y = yr;
     const f16x4 yb = f2h4(y.x, y.y, y.z, y.w);
     if (row >= M) return;
-    f16* dst = (which == 0 ? q : k) + ((long)head * rows + row) * 64 + d;
-    *reinterpret_cast<f16x4*>(dst) = yb;
+    // q / k: [heads][rows][64], addressed by 32-bit byte offsets (the launcher checks the range)
+    buffer_st_f16x4(buffer_over(which ? k : q, (uint32_t)dim * rows * 2),
+                    (uint32_t)((head * rows + row) * 64 + d) * 2, yb);
   }
 };
 
@@ -898,6 +924,7 @@ hipError_t gemm_qkv_rope(const f16* A, int lda, const f16* W, int ldw, const flo
                          f16* vt, int rp, hipStream_t stream, const int32_t* m_live) {
   (void)heads;
   if (rp < M) return hipErrorInvalidValue;
+  if ((long)dim * rp * 2 >= (1L << 31)) return hipErrorInvalidValue;  // q / k buffer offsets
   return launch(A, lda, W, ldw, M, 3 * dim, dim,
                 EpiQkvRope{bias, dim, rp, pos, rope_cos, rope_sin, rope_dim, max_pos, q, k, vt, rp},
                 stream, m_live);
