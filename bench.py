@@ -316,6 +316,111 @@ def token2wav_leg(fcv, est, batch, dev) -> dict:
             "timing": "wall clock with torch.cuda.synchronize() on both sides, best of 2"}
 
 
+def chunk_plans(prompt_tokens: int, total: int, chunk: int = 15, lookahead: int = 3,
+                scale: int = 2) -> list[tuple[int, int, bool]]:
+    """(prefix_len, token_offset, finalize) of every chunk of a session whose tokens all arrive
+    before token2wav asks for them, by the reference's planner rules (streaming/chunker.py:
+    20-56): the first hop is ``chunk`` tokens plus the pad that aligns the prompt to a multiple
+    of ``chunk``; each chunk also reads ``lookahead`` tokens it does not consume; the hop then
+    grows by ``scale`` up to four times ``chunk``; what is left at the end is one final chunk."""
+    pad = (-prompt_tokens) % chunk if prompt_tokens > 0 else 0
+    hop, done, plans = chunk, 0, []
+    while True:
+        this = hop + (pad if done == 0 else 0)
+        if total - done < this + lookahead:
+            break
+        plans.append((done + this + lookahead, done, False))
+        done += this
+        hop = min(4 * chunk, max(chunk, hop * scale))
+    if total > done:
+        plans.append((total, done, True))
+    return plans
+
+
+def stream_leg(fcv, est, batch, dev) -> dict:
+    """Packed streaming steps (token2wav.py:203-226 with the packed vocoder): the workload's
+    requests as concurrent sessions, every session's next chunk in one
+    ``StreamingFlow.stream_step_batched`` call (front-end over the full token prefix, the
+    chunk-causal 10-step CFG solve from the fixed noise prefix on the 22-block estimator, one
+    packed HiFT call over the sessions' Mel caches), until every session has emitted its final
+    chunk.  Wall time of each step between device synchronisations, on a second pass over fresh
+    sessions (the first, untimed, captures the capacity graphs); plus one session's first chunk
+    alone, the token2wav share of a time-to-first-packet at concurrency 1."""
+    import copy
+    from types import SimpleNamespace
+
+    import torch
+    fdims = fcv.synthetic.FlowDims()
+    fe = fcv.FlowFrontEnd(device=dev)
+    fe.load_reference_state_dict(fcv.synthetic.random_flow_state_dict(fdims, seed=0))
+    fe.finalize_weights()
+    fe.decoder = fcv.CFMDecoder(est)
+    hdims = fcv.synthetic.HiFTDims()
+    p_tok = [p // 2 for p in batch.prompt_lengths]
+    n_tok = [max(1, (n - p) // 2) for n, p in zip(batch.lengths, batch.prompt_lengths)]
+    voc = fcv.HiFTVocoder(hdims, device=dev, buffers=fcv.synthetic.random_hift_buffers(
+        hdims, max_samples=hdims.upsample_scale * 2 * max(n_tok), seed=1))
+    voc.load_reference_state_dict(fcv.synthetic.random_hift_state_dict(hdims, seed=0))
+    voc.finalize_weights()
+    sf = fcv.StreamingFlow(fe, vocoder=voc.inference)
+    g = torch.Generator().manual_seed(8)
+    sessions = []
+    for p, n in zip(p_tok, n_tok):
+        cond = SimpleNamespace(
+            prompt_tokens_flow=torch.randint(0, fdims.vocab, (p,), generator=g).tolist(),
+            prompt_feat=torch.randn(1, 2 * p, 80, generator=g),
+            spk_embedding=torch.randn(192, generator=g))
+        sessions.append(SimpleNamespace(
+            cond=cond, tokens=torch.randint(0, fdims.vocab, (n,), generator=g).tolist(),
+            mel_cache=None, speech_offset=0, chunk_index=0))
+    plans = [[SimpleNamespace(prefix_len=a, token_offset=b, finalize=c)
+              for a, b, c in chunk_plans(p, n)] for p, n in zip(p_tok, n_tok)]
+
+    def run(timed: bool):
+        live = copy.deepcopy(sessions)
+        step_ms, samples = [], 0
+        for k in range(max(len(pl) for pl in plans)):
+            idx = [i for i, pl in enumerate(plans) if k < len(pl)]
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            pcm = sf.stream_step_batched([live[i] for i in idx], [plans[i][k] for i in idx])
+            torch.cuda.synchronize()
+            step_ms.append((time.perf_counter() - t0) * 1e3)
+            samples += sum(x.shape[-1] for x in pcm)
+        return step_ms, samples
+
+    run(False)
+    step_ms, samples = run(True)
+
+    def first_alone() -> float:
+        s = copy.deepcopy(sessions[0])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        sf.stream_step(s, plans[0][0])
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3
+
+    first_alone()
+    alone = sorted(first_alone() for _ in range(3))[1]
+    total_ms = sum(step_ms)
+    audio = samples / hdims.sampling_rate
+    return {"what": "packed streaming steps, tokens -> PCM: front-end over each session's full "
+                    "token prefix, chunk-causal 10-step CFG solve (22 blocks) from the fixed "
+                    "noise prefix, one packed HiFT call over the sessions' Mel caches",
+            "sessions": len(sessions), "prompt_tokens": p_tok, "tokens": n_tok,
+            "chunk_plan": "15-token first hop plus the prompt-alignment pad, 3 lookahead "
+                          "tokens, hop doubling to 60, final remainder "
+                          "(streaming/chunker.py:20-56); all tokens available up front",
+            "steps": len(step_ms), "step_ms": [round(v, 2) for v in step_ms],
+            "ms_total": round(total_ms, 2), "audio_seconds": round(audio, 2),
+            "audio_seconds_per_second": round(audio / (total_ms * 1e-3), 1),
+            "first_chunk_ms": {"packed_sessions": round(step_ms[0], 2),
+                               "one_session_alone": round(alone, 2)},
+            "timing": "wall clock with torch.cuda.synchronize() around each step; the second "
+                      "pass over fresh copies of the sessions (the first captures graphs); "
+                      "one session alone: median of 3 after one untimed call"}
+
+
 def _group_caps(fcv, b) -> tuple:
     """Capacity bucket of each request group the solver makes of batch `b`."""
     groups = fcv.solver.request_groups(b.lengths, fcv.solver.default_concurrency(b.n_requests))
@@ -418,6 +523,8 @@ def main() -> int:
     ap.add_argument("--no-hift", action="store_true", help="skip the HiFT vocoder leg")
     ap.add_argument("--no-token2wav", action="store_true",
                     help="skip the end-to-end tokens -> waveform leg")
+    ap.add_argument("--no-stream", action="store_true",
+                    help="skip the packed streaming-step leg (tokens -> PCM chunks)")
     ap.add_argument("--eager", action="store_true", help="launch kernels one by one (no hipGraph)")
     ap.add_argument("--no-fresh-layouts", action="store_true",
                     help="skip the leg that solves new layouts through the bucket's graph")
@@ -563,6 +670,11 @@ def main() -> int:
         log("[bench] Token2Wav pass (tokens -> waveform)")
         t2w = token2wav_leg(fcv, est, batch, dev)
 
+    stream_res = None
+    if not args.no_stream:
+        log("[bench] packed streaming steps (tokens -> PCM chunks)")
+        stream_res = stream_leg(fcv, est, batch, dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (fp32 oracle, padded SDPA)")
@@ -626,6 +738,7 @@ def main() -> int:
         "frontend": frontend,
         "hift": hift,
         "token2wav": t2w,
+        "stream": stream_res,
         "eager_ms_per_step": round(eager_wall * 1e3 / K, 4),
         "eager_timing": (f"median of 3 eager {K}-step solves with the replays' request groups, "
                          "each between torch.cuda.synchronize() calls"),
